@@ -1,0 +1,51 @@
+// testkit.hip -- seeded synthetic K/V for tests and benchmarks (gfx950).
+//
+// Not part of the reference interface: the reference fills its cache from a
+// model; the benchmarks here need tens of GB of N(0,1) fp16 K/V resident in
+// HBM without a host round trip.  Element e of a fill gets
+//     u = splitmix64(seed + e * 0x9E3779B97F4A7C15)
+//     x = sqrt(-2 ln u1) * cos(2 pi u2)    (Box-Muller, u1,u2 from the two halves)
+// rounded to fp16 (RNE).  Tests never regenerate these values on the host:
+// they download what the device holds, so the device math need not match libm.
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+#include "check.h"
+#include "hal.h"
+
+namespace {
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__global__ void fill_normal_f16_kernel(uint16_t* __restrict__ p, uint64_t n, uint64_t seed, float scale) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t e = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; e < n; e += stride) {
+        const uint64_t u = splitmix64(seed ^ (e * 0x9E3779B97F4A7C15ull));
+        const float u1 = ((float)(uint32_t)(u >> 40) + 0.5f) * (1.0f / 16777216.0f);
+        const float u2 = (float)(uint32_t)(u & 0xFFFFFFu) * (1.0f / 16777216.0f);
+        const float x = sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2) * scale;
+        const _Float16 h = (_Float16)x;
+        p[e] = __builtin_bit_cast(uint16_t, h);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+// Fill n fp16 values at p with seeded N(0, scale^2) draws.
+void testkit_fill_normal_f16(uint16_t* p, uint64_t n, uint64_t seed, float scale, nova_stream_t s) {
+    if (n == 0) return;
+    uint64_t blocks = (n + 255) / 256;
+    if (blocks > 1u << 20) blocks = 1u << 20;
+    hipLaunchKernelGGL(fill_normal_f16_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(s), p, n, seed, scale);
+    NOVA_LAUNCHED();
+}
+
+}  // extern "C"

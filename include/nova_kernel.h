@@ -1,0 +1,123 @@
+/*
+ * nova_kernel.h -- kernel-layer entry points of the paged KV-cache path (C ABI).
+ *
+ * One shared library per model geometry (libnova_hip_<model>.so), exactly as
+ * the reference welds NH / NKV / HD / L and the page size at compile time
+ * (include/nova/model/select.h:6-32, code/graph/kv_pool_cfg.h:12-33): there is
+ * no runtime shape argument.  nova_model_geometry() reports what a library was
+ * built for.
+ *
+ * Pool layout (unchanged from the reference, include/nova/model.h:140-145,
+ * code/graph/kv_pool.h:8-15): separate K and V pools, each
+ *     pool[layer][NB][KB][NKV][HD],  KB = 16 tokens per page,
+ * address of token pos of a session = ((layer*NB + table[pos>>4])*KB + (pos&15))*NKV*HD.
+ * K/V elements are IEEE fp16 bit patterns (uint16_t); the reference stores fp32
+ * (dense.h:25-26), the build stores fp16.  Q and O stay fp32.
+ *
+ * All launches are asynchronous on the given stream and return nothing; bad
+ * arguments abort before anything is launched (include/nova/config.h:42-63).
+ */
+#ifndef NOVA_KERNEL_H
+#define NOVA_KERNEL_H
+#include <stddef.h>
+#include <stdint.h>
+#include "hal.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Geometry the library was compiled for.  Not a reference surface: the
+ * reference reads it from ActiveModel (select.h); an FFI needs it as a call. */
+typedef struct {
+    int nh, nkv, hd, n_layers, kv_block, max_split;
+    const char* name;
+} nova_geometry;
+nova_geometry nova_model_geometry(void);
+
+/* Append n tokens of K and V at logical positions pos0..pos0+n-1.
+ * k, v: [n][NKV][HD] fp16.  table: the session's device block table.
+ * Replaces nova::launch_kv_store_paged, include/nova/kernel.h:44-45
+ * (kernel src/kernel/elem.cu:59-76, launcher :93-98). */
+void launch_kv_store_paged(uint16_t* pool_k, uint16_t* pool_v, const int32_t* table, int layer, int nb,
+                           int n, int64_t pos0, const uint16_t* k, const uint16_t* v, nova_stream_t s);
+
+/* Single-session split-K decode over keys [0, n_keys) of one layer.
+ * q, o: [NH][HD] fp32.  scratch: caller-owned, >= NH*32*(HD+2) floats
+ * (src/model.cpp:114,148).  Replaces nova::launch_attn_decode_paged,
+ * include/nova/kernel.h:62-64 (attn.cu:197-289 + combine :163-191, launcher :498-512). */
+void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint16_t* pool_v,
+                              const int32_t* table, int layer, int nb, int n_keys,
+                              float* o, float* scratch, nova_stream_t s);
+
+/* Causal attention of n_q new queries at positions n_past..n_past+n_q-1 over
+ * keys [0, n_past+qi] (the chunk must already be appended).  q, o:
+ * [n_q][NH][HD] fp32.  Replaces nova::launch_attn_prefill_paged,
+ * include/nova/kernel.h:65-67 (attn.cu:293-357, launcher :514-525). */
+void launch_attn_prefill_paged(const float* q, const uint16_t* pool_k, const uint16_t* pool_v,
+                               const int32_t* table, int layer, int nb,
+                               int n_q, int n_past, float* o, nova_stream_t s);
+
+/* ---------------- extensions (no single reference counterpart) ---------------- */
+
+/* Batched ragged decode: one launch for all sessions of a layer, optionally
+ * fused with that layer's 1-token append.  Replaces the 2N per-session
+ * launches of Engine::decode_batch (src/model.cpp:282-289).
+ *   q, o     [n_sess][NH][HD] fp32
+ *   tables   session i's block table is tables + i*table_stride (the
+ *            reference keeps all tables in one array, model.cpp:95)
+ *   n_keys   device int32[n_sess]; keys [0, n_keys[i]) are attended
+ *   k_new, v_new  NULL, or [n_sess][NKV][HD] fp16: the token at position
+ *            n_keys[i]-1 is written into the pool AND attended from these
+ *            buffers in the same launch (append-then-attend, dense.h:75-95)
+ *   workspace    from attn_decode_batch_workspace_bytes(); its 4*n_sess
+ *            counter bytes at the start must be zero before the first call
+ *            (dev_zero once); every call leaves them zero again.
+ * n_keys[i] == 0 yields a zero output row. */
+size_t attn_decode_batch_workspace_bytes(int n_sess);
+void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* pool_v,
+                                    const int32_t* tables, int table_stride, const int32_t* n_keys,
+                                    int n_sess, int layer, int nb,
+                                    const uint16_t* k_new, const uint16_t* v_new,
+                                    float* o, void* workspace, nova_stream_t s);
+
+/* Batched chunked-prefill attention: n_sess sessions each with a chunk of n_q
+ * queries at positions n_past[i]..n_past[i]+n_q-1 (device int32[n_sess]).
+ * q, o: [n_sess][n_q][NH][HD] fp32; tables as for the batched decode.  One
+ * launch instead of n_sess launch_attn_prefill_paged calls. */
+void launch_attn_prefill_paged_batch(const float* q, const uint16_t* pool_k, const uint16_t* pool_v,
+                                     const int32_t* tables, int table_stride, const int32_t* n_past,
+                                     int n_sess, int n_q, int layer, int nb, float* o, nova_stream_t s);
+
+/* Batched copy-on-write page copy: for every pair c, copy page src[c] to page
+ * dst[c] in every layer of both pools (n_layers*2 pages per pair, one launch).
+ * src/dst are device int32[n_pairs].  Replaces the 2L cudaMemcpyAsync calls of
+ * Engine::cow_guard, src/model.cpp:178-187. */
+void launch_kv_cow_copy(uint16_t* pool_k, uint16_t* pool_v, int nb, const int32_t* src,
+                        const int32_t* dst, int n_pairs, nova_stream_t s);
+
+/* Apply a batch of COW decisions in one launch: for each op, copy page src to
+ * page dst in every layer of both pools, then set tables_dev[table_index] = dst.
+ * ops is a HOST array (copied into the launch, 64 ops per kernel), so no
+ * staging buffer or host sync is needed: the fused form of cow_guard's
+ * 2L+1 copies (src/model.cpp:171-191) for any number of sessions. */
+typedef struct { int32_t src, dst; int64_t table_index; } nova_cow_op;
+void launch_kv_cow_apply(uint16_t* pool_k, uint16_t* pool_v, int nb, int32_t* tables_dev,
+                         const nova_cow_op* ops, int n_ops, nova_stream_t s);
+
+/* Clear pages (all layers, K and V) -- the per-page memsets of
+ * SessionManager::create, code/session.h:107-118, as one launch.
+ * pages: device int32[n_pages]. */
+void launch_kv_zero_pages(uint16_t* pool_k, uint16_t* pool_v, int nb, const int32_t* pages,
+                          int n_pages, nova_stream_t s);
+
+/* Update single entries of device block tables: table_dev[idx[c]] = val[c]
+ * for c < n (idx/val are device int32).  The H2D table patch of cow_guard
+ * (model.cpp:188-190) for a whole batch of COWs. */
+void launch_table_patch(int32_t* table_dev, const int32_t* idx, const int32_t* val, int n,
+                        nova_stream_t s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

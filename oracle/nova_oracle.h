@@ -1,0 +1,124 @@
+/*
+ * nova_oracle.h -- CPU oracle for the paged KV-cache path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is a plain-C restatement of the
+ * reference algorithms (Conflux Nova, CUDA line) and exists to check the HIP
+ * product.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it, and only as the checker / the timed CPU baseline; the
+ * product library never links or calls it.
+ *
+ * Every function names the reference file:line it restates (paths relative to
+ * the reference repository root).  Shapes are runtime arguments here (the
+ * reference welds them at compile time); K/V are fp16 bit patterns widened to
+ * fp32, Q/O are fp32, accumulation is fp32 unless the name says f64.
+ */
+#ifndef NOVA_ORACLE_H
+#define NOVA_ORACLE_H
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------- geometry ---------------- */
+typedef struct {
+    int nh;   /* query heads              */
+    int nkv;  /* kv heads                 */
+    int hd;   /* head dim (64 or 128)     */
+    int kb;   /* tokens per page (8..64)  */
+} or_geom;
+
+/* ---------------- fp16 helpers ---------------- */
+float    or_f16_to_f32(uint16_t h);
+uint16_t or_f32_to_f16(float f);                 /* round-to-nearest-even */
+void     or_f32_to_f16_n(const float* src, uint16_t* dst, size_t n);
+void     or_f16_to_f32_n(const uint16_t* src, float* dst, size_t n);
+
+/* ---------------- KvPool (code/graph/kv_pool.h:68-197) ---------------- */
+typedef struct or_pool or_pool;
+or_pool* or_pool_new(int n_slices, int64_t ctx);             /* KvPool::init   :70-84  */
+void     or_pool_delete(or_pool* p);
+int      or_pool_acquire(or_pool* p);                        /* :90-113, returns slice id or -1 */
+int      or_pool_alloc_block(or_pool* p);                    /* :116-122 */
+void     or_pool_free_block(or_pool* p, int b);              /* :123-126 */
+void     or_pool_ref_block(or_pool* p, int b);               /* :127 */
+int      or_pool_refcnt(const or_pool* p, int b);            /* :128 */
+void     or_pool_attach(or_pool* p, int dst, int src, int k);              /* :132-138 */
+void     or_pool_attach_prefix(or_pool* p, int dst, int src, int64_t n);  /* :141-148 */
+int      or_pool_cow_slice(or_pool* p, int s, int64_t pos);  /* :153-166 */
+void     or_pool_release(or_pool* p, int s);                 /* :168-174 */
+int      or_pool_nblocks(const or_pool* p);
+int      or_pool_nb_total(const or_pool* p);
+int      or_pool_cow_count(const or_pool* p);
+int      or_pool_free_blocks(const or_pool* p);
+int      or_pool_used(const or_pool* p);
+int      or_pool_free_slices(const or_pool* p);
+/* state export for bit-exact comparisons */
+int      or_pool_free_list(const or_pool* p, int* out, int cap);  /* free-block stack, bottom..top */
+int      or_pool_refcnts(const or_pool* p, int* out, int cap);
+int      or_pool_table(const or_pool* p, int s, int32_t* out, int cap);
+int64_t  or_pool_n_past(const or_pool* p, int s);
+void     or_pool_set_n_past(or_pool* p, int s, int64_t n);
+int      or_pool_need_copy(const or_pool* p, int s, int* from, int* blk);
+
+/* ---------------- kv_block IDs (code/graph/kv_block.h:21-83) ---------------- */
+uint64_t or_kv_hash_ids(const int* ids, size_t n);           /* :21-64 */
+uint64_t or_kv_hash_text(const char* text, size_t n);        /* :67-72 */
+void     or_kv_hash_hex(uint64_t v, char out[17]);           /* :74-79 */
+void     or_kv_block_id(uint64_t prefix, uint64_t suffix, char out[40]);  /* :81-83 */
+
+/* ---------------- BlockRegistry (code/graph/kv_registry.h:26-66) ---------------- */
+typedef struct or_registry or_registry;
+or_registry* or_registry_new(void);
+void     or_registry_delete(or_registry* r);
+void     or_registry_set_capacity(or_registry* r, size_t n);
+void     or_registry_put(or_registry* r, uint64_t prefix, uint64_t suffix, int session, int turn,
+                         int64_t pos0, int64_t pos1);
+int      or_registry_find(const or_registry* r, uint64_t prefix, uint64_t suffix,
+                          int* session, int* turn, int64_t* pos0, int64_t* pos1);
+int      or_registry_live(const or_registry* r);
+int      or_registry_total(const or_registry* r);
+
+/* ---------------- paged append (src/kernel/elem.cu:59-76,93-98) ---------------- */
+void or_kv_store_paged(or_geom g, uint16_t* pool_k, uint16_t* pool_v, const int32_t* table,
+                       int layer, int nb, int n, int64_t pos0,
+                       const uint16_t* k, const uint16_t* v);
+/* gather logical positions [0,n) of one layer into contiguous [n][nkv][hd] */
+void or_kv_gather_paged(or_geom g, const uint16_t* pool, const int32_t* table, int layer, int nb,
+                        int64_t n, uint16_t* out);
+
+/* ---------------- COW page copy (src/model.cpp:171-191) ---------------- */
+void or_cow_copy(or_geom g, uint16_t* pool_k, uint16_t* pool_v, int n_layers, int nb,
+                 int src, int dst);
+
+/* ---------------- attention ----------------
+ * decode: fa_split_paged_kernel + fa_combine_kernel (src/kernel/attn.cu:163-289),
+ * split rule of launch_attn_decode_paged (attn.cu:498-512); emulates the 4-warp
+ * ranges, the per-lane fma order and the shuffle-down reduction order.
+ * q [nh][hd] f32, o [nh][hd] f32. */
+void or_attn_decode_paged(or_geom g, const float* q, const uint16_t* pool_k, const uint16_t* pool_v,
+                          const int32_t* table, int layer, int nb, int n_keys, float* o);
+/* textbook two-pass softmax attention in double (tests/sycl_bench.cpp:889-943 form) */
+void or_attn_decode_paged_f64(or_geom g, const float* q, const uint16_t* pool_k, const uint16_t* pool_v,
+                              const int32_t* table, int layer, int nb, int n_keys, double* o);
+/* prefill: flash_paged_kernel<false> (attn.cu:293-357): one (query, head) at a time,
+ * causal keys [0, n_past+qi].  q/o [n_q][nh][hd]. */
+void or_attn_prefill_paged(or_geom g, const float* q, const uint16_t* pool_k, const uint16_t* pool_v,
+                           const int32_t* table, int layer, int nb, int n_q, int n_past, float* o);
+void or_attn_prefill_paged_f64(or_geom g, const float* q, const uint16_t* pool_k,
+                               const uint16_t* pool_v, const int32_t* table, int layer, int nb,
+                               int n_q, int n_past, double* o);
+
+/* Batched decode over sessions for the CPU baseline: session i uses
+ * tables + i*table_stride and n_keys[i]; q/o [n_sess][nh][hd].  Work units
+ * (session, head) are spread over n_threads pthreads.  Same arithmetic as
+ * or_attn_decode_paged. */
+void or_attn_decode_batch(or_geom g, const float* q, const uint16_t* pool_k, const uint16_t* pool_v,
+                          const int32_t* tables, int table_stride, const int32_t* n_keys, int n_sess,
+                          int layer, int nb, float* o, int n_threads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,573 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged KV-cache hot path on one MI355X.
+
+Default workload (the headline metric): Qwen2.5-7B attention
+geometry (28 query heads, 4 kv heads, head_dim 128, 28 layers), fp16 K/V in
+16-token pages, 16 sessions with context lengths uniform in [512, 8192]
+(seeded), pages scattered by a seeded shuffle of a shared pool.  One step =
+for each of the 28 layers: append 1 token per session, then split-K paged
+attention for all sessions -- one fused launch per layer
+(launch_attn_decode_paged_batch with k_new/v_new), the 28 launches replayed
+from a HIP graph.  Inputs (pool, tables, Q, new K/V for every layer) are
+resident in HBM before timing starts.  The appended position is the same each
+step (slot ctx_i of session i is rewritten), so every step does identical work.
+
+Output: one JSON line (metric = KV GB/s; ms_per_step; roofline of the decode
+kernel measured with HIP events; cpu_baseline = the C oracle on the host cores
+over one layer of the same workload).
+
+Other workloads (--workload): single1p5b (config 1), cow (config 3),
+longctx14b (config 4), prefill (config 5).  They print their own JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "conflux-nova_amd"))
+sys.path.insert(0, str(ROOT / "oracle"))
+
+import nova_amd  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E vendor peak
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA vendor peak
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="decode7b",
+                    choices=["decode7b", "single1p5b", "cow", "longctx14b", "prefill"])
+    ap.add_argument("--seed", type=int, default=2024)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
+    return ap.parse_args()
+
+
+def cpu_threads(args) -> int:
+    if args.cpu_threads:
+        return args.cpu_threads
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+class Timer:
+    """HIP events on a given stream."""
+
+    def __init__(self, nova, stream):
+        self.n, self.s = nova, stream
+        self.a, self.b = nova.dev_event_create(), nova.dev_event_create()
+
+    def start(self):
+        self.n.dev_event_record(self.a, self.s)
+
+    def stop(self) -> float:
+        self.n.dev_event_record(self.b, self.s)
+        return self.n.dev_event_elapsed_ms(self.a, self.b)
+
+
+def decode_bytes(n_keys, nkv, hd, nh, layers) -> int:
+    """Algorithmic HBM bytes of append + decode (per step, all layers)."""
+    n_keys = np.asarray(n_keys, np.int64)
+    per_layer = (n_keys * nkv * hd * 2 * 2            # K + V rows read (fp16)
+                 + nkv * hd * 2 * 2                   # appended K + V row written
+                 + 4 * ((n_keys + 15) // 16)          # block-table entries
+                 + nh * hd * 4 * 2)                   # Q read, O written (fp32)
+    return int(per_layer.sum()) * layers
+
+
+class DecodeWorkload:
+    """Ragged batched decode: pool, tables, per-layer Q / new K/V, graph."""
+
+    def __init__(self, nova, ctx, seed, stream, layers=None):
+        self.nova, self.s = nova, stream
+        self.layers = layers or nova.n_layers
+        rng = np.random.default_rng(seed)
+        self.ctx = np.asarray(ctx, np.int32)
+        self.n = len(ctx)
+        self.n_keys = (self.ctx + 1).astype(np.int32)          # append at pos ctx, attend ctx+1 keys
+        pages = (self.n_keys + 15) // 16
+        self.max_pages = int(pages.max())
+        self.nb = int(pages.sum()) + 8
+        perm = rng.permutation(self.nb).astype(np.int32)
+        tables = np.zeros((self.n, self.max_pages), np.int32)
+        off = 0
+        for i in range(self.n):
+            tables[i, :pages[i]] = perm[off:off + pages[i]]
+            off += pages[i]
+        self.tables_h = tables
+        page_halves = nova.kb * nova.kvw
+        self.layer_halves = self.nb * page_halves
+        per_pool = nova.n_layers * self.layer_halves
+        self.k = nova.alloc(per_pool * 2)
+        self.v = nova.alloc(per_pool * 2)
+        nova.testkit_fill_normal_f16(self.k.ptr, per_pool, seed * 7 + 1, 1.0, stream)
+        nova.testkit_fill_normal_f16(self.v.ptr, per_pool, seed * 7 + 2, 1.0, stream)
+        self.tables = nova.upload(tables)
+        self.nk = nova.upload(self.n_keys)
+        L = self.layers
+        self.q_h = rng.standard_normal((L, self.n, nova.nh, nova.hd)).astype(np.float32)
+        self.knew_h = rng.standard_normal((L, self.n, nova.nkv, nova.hd)).astype(np.float16).view(np.uint16)
+        self.vnew_h = rng.standard_normal((L, self.n, nova.nkv, nova.hd)).astype(np.float16).view(np.uint16)
+        self.q = nova.upload(self.q_h)
+        self.knew = nova.upload(self.knew_h)
+        self.vnew = nova.upload(self.vnew_h)
+        self.o = nova.alloc(L * self.n * nova.nh * nova.hd * 4)
+        self.ws = nova.alloc(nova.attn_decode_batch_workspace_bytes(self.n))
+        nova.dev_zero(self.ws.ptr, self.ws.nbytes, stream)
+        nova.dev_stream_sync(stream)
+        self.graph = None
+
+    def launch_layer(self, l):
+        nv = self.nova
+        qs = self.n * nv.nh * nv.hd
+        kvs = self.n * nv.kvw
+        nv.launch_attn_decode_paged_batch(
+            self.q.ptr + l * qs * 4, self.k.ptr, self.v.ptr, self.tables.ptr, self.max_pages, self.nk.ptr,
+            self.n, l, self.nb, self.knew.ptr + l * kvs * 2, self.vnew.ptr + l * kvs * 2,
+            self.o.ptr + l * qs * 4, self.ws.ptr, self.s)
+
+    def step_eager(self):
+        for l in range(self.layers):
+            self.launch_layer(l)
+
+    def capture(self):
+        nv = self.nova
+        nv.dev_graph_begin(self.s)
+        self.step_eager()
+        self.graph = nv.dev_graph_end(self.s)
+
+    def step(self):
+        self.nova.dev_graph_launch(self.graph, self.s)
+
+    def bytes_per_step(self) -> int:
+        nv = self.nova
+        return decode_bytes(self.n_keys, nv.nkv, nv.hd, nv.nh, self.layers)
+
+    def kernel_ms(self, reps=3) -> float:
+        """average duration of one decode launch, HIP events around each launch"""
+        t = Timer(self.nova, self.s)
+        total, cnt = 0.0, 0
+        for _ in range(reps):
+            for l in range(self.layers):
+                t.start()
+                self.launch_layer(l)
+                total += t.stop()
+                cnt += 1
+        return total / cnt
+
+    def cpu_sample(self, layer, threads):
+        """Run the C oracle on the host over one layer; returns (seconds, outputs)."""
+        from oracle_py import Oracle
+        nv = self.nova
+        orc = Oracle()
+        shape = (self.nb, nv.kb, nv.nkv, nv.hd)
+        off = layer * self.layer_halves * 2
+        pk = nv.download(self.k.ptr + off, shape, np.uint16)
+        pv = nv.download(self.v.ptr + off, shape, np.uint16)
+        # the appended token is part of the layer's keys
+        for i in range(self.n):
+            orc.kv_store_paged(nv.model, pk, pv, np.ascontiguousarray(self.tables_h[i]), 0, self.nb, 1,
+                               int(self.ctx[i]), np.ascontiguousarray(self.knew_h[layer, i]),
+                               np.ascontiguousarray(self.vnew_h[layer, i]))
+        q = np.ascontiguousarray(self.q_h[layer])
+        t0 = time.perf_counter()
+        out = orc.attn_decode_batch(nv.model, q, pk, pv, self.tables_h, self.n_keys, 0, self.nb, threads)
+        return time.perf_counter() - t0, out
+
+
+def ragged_ctx(seed, n, lo, hi):
+    return np.random.default_rng(seed).integers(lo, hi + 1, n).astype(np.int32)
+
+
+def load_traffic(name: str):
+    """HBM bytes per launch from the committed rocprofv3 PMC summary, if any."""
+    p = ROOT / "profiles" / f"{name}_traffic.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text()).get("traffic_bytes_per_launch")
+        except (OSError, ValueError):
+            return None
+    return None
+
+
+def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
+    nova = nova_amd.load(model)
+    s = nova.dev_stream_create()
+    wl = DecodeWorkload(nova, ctx, args.seed, s)
+    wl.step_eager()            # first touch, check launches
+    nova.dev_stream_sync(s)
+    wl.capture()
+    for _ in range(args.warmup):
+        wl.step()
+    nova.dev_stream_sync(s)
+    t = Timer(nova, s)
+    nova.dev_sync()
+    t.start()
+    for _ in range(args.steps):
+        wl.step()
+    ms = t.stop() / args.steps
+    nova.dev_sync()
+    bytes_step = wl.bytes_per_step()
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    k_ms = wl.kernel_ms()
+    bytes_launch = bytes_step / wl.layers
+    achieved = bytes_launch / (k_ms * 1e-3) / 1e9
+    traffic = load_traffic(workload_name)
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": "decode_kernel<true> (launch_attn_decode_paged_batch)",
+            "kernel_us": round(k_ms * 1e3, 2), "bytes_per_launch": bytes_launch}
+    cpu = None
+    if not args.no_cpu:
+        th = cpu_threads(args)
+        secs, out = wl.cpu_sample(0, th)
+        # parity at full size on layer 0 (GPU output of the last replay)
+        got = nova.download(wl.o, (wl.n, nova.nh, nova.hd), np.float32)
+        err = float(np.abs(got - out).max())
+        cpu_gbs = (bytes_step / wl.layers) / secs / 1e9
+        cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": th, "kind": "port",
+               "sample": f"1 of {wl.layers} layers ({cpu_scale_note}); C oracle or_attn_decode_batch, "
+                         f"{secs:.2f} s; max|gpu-cpu| on that layer {err:.2e}",
+               "us_per_step_equiv": round(secs * wl.layers * 1e6, 1)}
+    line = {
+        "metric": metric_cfg["metric"], "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "us_per_step": round(ms * 1e3, 2), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16 KV / f32 accumulate",
+        "data": "synthetic (seeded N(0,1) K/V, Q; seeded ragged contexts and page shuffle)",
+        "config": metric_cfg["config"], "roofline": roof, "cpu_baseline": cpu,
+    }
+    return line
+
+
+# ---------------------------------------------------------------------------
+# config 3: copy-on-write prefix sharing
+# ---------------------------------------------------------------------------
+VOCAB = 151936
+ROOT_LEN = 2048
+FORK = 2047           # unaligned fork point: with 16-token pages a 2048-token fork never COWs
+N_ROOTS, PER_ROOT = 4, 16
+
+
+def run_cow(args):
+    """4 roots x 2048 seeded token ids, 64 children forked at 2047 tokens, each
+    appending a divergent suffix of U[0,1024] tokens token by token.  The first
+    append of every child copies the shared, half-filled tail page (all 28
+    layers, K and V); the timed figure is that batched COW copy.  Block tables,
+    refcounts, free list, cow_count and the kv_block IDs are compared with the C
+    oracle driven by the same calls."""
+    import ctypes as C
+    from oracle_py import Oracle
+    nova = nova_amd.load("qwen25_7b")
+    orc = Oracle()
+    rng = np.random.default_rng(args.seed)
+    n_child = N_ROOTS * PER_ROOT
+    suffix = rng.integers(0, 1025, n_child)
+    order = np.argsort(-suffix, kind="stable")          # children created longest-suffix first
+    suffix = suffix[order]
+    ctx = ROOT_LEN + 1024
+    n_slices = N_ROOTS + n_child + 4                     # 4 spare slices feed alloc_block
+    h = nova.nova_paged_new(n_slices, ctx)
+    pool = nova.nova_paged_pool(h)
+    nb = nova.nova_paged_nb(h)
+    nblocks = nova.nova_kvpool_nblocks(pool)
+    st = nova.nova_paged_stream(h)
+    kp, vp = nova.nova_paged_pool_k(h), nova.nova_paged_pool_v(h)
+    oh = orc.pool.new(n_slices, ctx)
+    sess = [nova.nova_paged_create_session(h, 1) for _ in range(N_ROOTS + n_child)]
+    osess = [orc.pool.acquire(oh) for _ in range(N_ROOTS + n_child)]
+    assert sess == osess
+    per_pool = nova.n_layers * nb * nova.kb * nova.kvw
+    nova.testkit_fill_normal_f16(kp, per_pool, args.seed * 3 + 1, 1.0, st)
+    nova.testkit_fill_normal_f16(vp, per_pool, args.seed * 3 + 2, 1.0, st)
+    nova.dev_stream_sync(st)
+    # kv_block IDs: prefix = hash(root prompt up to the fork), suffix = hash(child ids) ^ 1
+    root_ids = rng.integers(0, VOCAB, (N_ROOTS, ROOT_LEN)).astype(np.int32)
+    child_ids = [rng.integers(0, VOCAB, int(L)).astype(np.int32) for L in suffix]
+
+    def nova_hash(ids):
+        a = np.ascontiguousarray(ids, dtype=np.int32)
+        return nova.nova_kv_hash_ids(a.ctypes.data_as(C.POINTER(C.c_int)), len(a))
+
+    ids_ok = True
+    reg, oreg = nova.nova_registry_new(), orc.registry.new()
+    for c in range(n_child):
+        root = c % N_ROOTS
+        p1, p2 = nova_hash(root_ids[root][:FORK]), orc.kv_hash_ids(root_ids[root][:FORK].tolist())
+        s1, s2 = nova_hash(child_ids[c]) ^ 1, orc.kv_hash_ids(child_ids[c].tolist()) ^ 1
+        ids_ok &= (p1 == p2) and (s1 == s2)
+        nova.nova_registry_put(reg, p1, s1, N_ROOTS + c, 1, FORK, FORK + int(suffix[c]))
+        orc.registry.put(oreg, p2, s2, N_ROOTS + c, 1, FORK, FORK + int(suffix[c]))
+    ids_ok &= nova.nova_registry_live(reg) == orc.registry.live(oreg)
+    # fork
+    layer0 = (nb, nova.kb, nova.nkv, nova.hd)
+    before_k = nova.download(kp, layer0, np.uint16)
+    for c in range(n_child):
+        child, root = N_ROOTS + c, c % N_ROOTS
+        nova.nova_paged_attach_prefix(h, child, root, FORK)
+        orc.pool.attach_prefix(oh, child, root, FORK)
+    # first append of every child: one batched COW (decisions in session order)
+    ids = (C.c_int * n_child)(*range(N_ROOTS, N_ROOTS + n_child))
+    pos = (C.c_int64 * n_child)(*([FORK] * n_child))
+    one = (C.c_int * n_child)(*([1] * n_child))
+    t = Timer(nova, st)
+    t.start()
+    copies = nova.nova_paged_cow_batch(h, ids, pos, one, n_child, st)
+    first_ms = t.stop()
+    for c in range(n_child):
+        orc.pool.cow_slice(oh, N_ROOTS + c, FORK)
+    # the same 64 page copies, repeated, for a stable per-launch time
+    lb = FORK >> 4
+    ops = (nova_amd.CowOp * n_child)()
+    for c in range(n_child):
+        child, root = N_ROOTS + c, c % N_ROOTS
+        ops[c].src = orc.pool.table_arr(oh, root)[lb]
+        ops[c].dst = orc.pool.table_arr(oh, child)[lb]
+        ops[c].table_index = child * nblocks + lb
+    for _ in range(args.warmup):
+        nova.launch_kv_cow_apply(kp, vp, nb, nova.nova_paged_tables(h), ops, n_child, st)
+    t.start()
+    for _ in range(args.steps):
+        nova.launch_kv_cow_apply(kp, vp, nb, nova.nova_paged_tables(h), ops, n_child, st)
+    cow_ms = t.stop() / args.steps
+    page_bytes = nova.n_layers * 2 * nova.kb * nova.kvw * 2
+    cow_bytes = n_child * 2 * page_bytes                 # read + write of every copied page
+    # suffix appends, token by token, all layers (children sorted: active ones are a prefix)
+    maxL = int(suffix.max())
+    kvn = nova.alloc(nova.n_layers * max(maxL, 1) * n_child * nova.kvw * 2 * 2)
+    nova.testkit_fill_normal_f16(kvn.ptr, nova.n_layers * max(maxL, 1) * n_child * nova.kvw * 2,
+                                 args.seed * 3 + 3, 1.0, st)
+    posbuf = nova.upload(np.full(n_child, FORK, np.int32))
+    tables_child = nova.nova_paged_tables(h) + N_ROOTS * nblocks * 4
+    extra_cow = 0
+    t.start()
+    for step in range(maxL):
+        active = int((suffix > step).sum())
+        act = (C.c_int * active)(*range(N_ROOTS, N_ROOTS + active))
+        ps = (C.c_int64 * active)(*([FORK + step] * active))
+        ns = (C.c_int * active)(*([1] * active))
+        extra_cow += nova.nova_paged_cow_batch(h, act, ps, ns, active, st)
+        for c in range(active):
+            orc.pool.cow_slice(oh, N_ROOTS + c, FORK + step)
+        pv = np.full(active, FORK + step, np.int32)
+        nova.dev_upload_async(posbuf.ptr, pv.ctypes.data, pv.nbytes, st)
+        nova.dev_stream_sync(st)
+        for l in range(nova.n_layers):
+            base = kvn.ptr + ((l * maxL + step) * n_child) * nova.kvw * 2 * 2
+            nova.launch_kv_store_paged_batch(kp, vp, tables_child, nblocks, posbuf.ptr, active, l, nb, 1,
+                                             base, base + n_child * nova.kvw * 2, st)
+    append_ms = t.stop()
+    nova.dev_stream_sync(st)
+    # ---- parity ----
+    from ctypes import c_int32
+    def prod_table(s_):
+        n = nova.nova_kvpool_table(pool, s_, None, 0)
+        buf = (c_int32 * n)()
+        nova.nova_kvpool_table(pool, s_, buf, n)
+        return list(buf)
+    def prod_free():
+        n = nova.nova_kvpool_free_list(pool, None, 0)
+        buf = (C.c_int * max(n, 1))()
+        nova.nova_kvpool_free_list(pool, buf, n)
+        return list(buf[:n])
+    tables_ok = all(prod_table(s_) == orc.pool.table_arr(oh, s_) for s_ in sess)
+    refcnt_ok = [nova.nova_kvpool_refcnt(pool, b) for b in range(nb)] == orc.pool.refcnt_arr(oh)
+    free_ok = prod_free() == orc.pool.free_list_arr(oh)
+    cow_ok = (copies == n_child and extra_cow == 0 and
+              nova.nova_kvpool_cow_count(pool) == orc.pool.cow_count(oh) == n_child)
+    dev_tables = nova.download(nova.nova_paged_tables(h), (n_slices, nblocks), np.int32)
+    dev_ok = all(dev_tables[s_].tolist() == orc.pool.table_arr(oh, s_) for s_ in sess)
+    # data: children see the donor prefix then their own suffix; donors untouched
+    after_k = nova.download(kp, layer0, np.uint16)
+    data_ok = True
+    kv_h = None
+    for c in (0, n_child // 2, n_child - 1):
+        child, root = N_ROOTS + c, c % N_ROOTS
+        L = int(suffix[c])
+        got = orc.kv_gather_paged("qwen25_7b", after_k, np.asarray(orc.pool.table_arr(oh, child), np.int32), 0, nb,
+                                  FORK + L)
+        want_prefix = orc.kv_gather_paged("qwen25_7b", before_k, np.asarray(orc.pool.table_arr(oh, root), np.int32),
+                                          0, nb, FORK)
+        data_ok &= np.array_equal(got[:FORK], want_prefix)
+        if L:
+            if kv_h is None:
+                # layer 0 block of each step: [K rows of all children][V rows of all children]
+                kv_h = nova.download(kvn, (maxL, 2, n_child, nova.nkv, nova.hd), np.uint16)
+            data_ok &= np.array_equal(got[FORK:], kv_h[:L, 0, c])
+    donor_ok = all(np.array_equal(after_k[p], before_k[p])
+                   for r_ in range(N_ROOTS) for p in orc.pool.table_arr(oh, r_)[:lb + 1])
+    nova.nova_paged_delete(h)
+    gbs = cow_bytes / (cow_ms * 1e-3) / 1e9
+    return {
+        "metric": "COW fork page copy GB/s (config 3, Qwen2.5-7B)", "value": round(gbs, 1), "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+        "dtype": "f16 KV (byte copy)", "data": "synthetic (seeded token ids, N(0,1) K/V)",
+        "config": {"workload": "config3: 4 roots x 2048 tokens, 64 children forked at 2047 tokens "
+                               "(unaligned, so the half-filled tail page is shared), suffix U[0,1024] "
+                               "appended token by token", "fork_tokens": FORK, "children": n_child,
+                   "suffix_tokens_total": int(suffix.sum())},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic("cow"),
+                     "kernel": "cow_apply_kernel (launch_kv_cow_apply)", "kernel_us": round(cow_ms * 1e3, 2),
+                     "bytes_per_launch": cow_bytes},
+        "first_cow_batch_us": round(first_ms * 1e3, 2),
+        "append_ms_total": round(append_ms, 1), "append_steps": maxL,
+        "parity": {"tables": tables_ok, "device_tables": dev_ok, "refcounts": refcnt_ok, "free_list": free_ok,
+                   "cow_once_per_child": cow_ok, "kv_block_ids": bool(ids_ok), "data": bool(data_ok),
+                   "donor_untouched": bool(donor_ok)},
+        "cpu_baseline": None,
+    }
+
+
+# ---------------------------------------------------------------------------
+# config 5: chunked prefill append + causal paged attention (MFMA)
+# ---------------------------------------------------------------------------
+def prefill_flops(n_past, n_q, nh, hd) -> int:
+    n_past = np.asarray(n_past, np.int64)
+    keys = n_past * n_q + n_q * (n_q + 1) // 2          # sum over q of (P + q + 1)
+    return int((keys * nh * 4 * hd).sum())
+
+
+def run_prefill(args):
+    nova = nova_amd.load("qwen25_7b")
+    s = nova.dev_stream_create()
+    rng = np.random.default_rng(args.seed)
+    n_sess, n_q = 8, 512
+    n_past = rng.integers(0, 4097, n_sess).astype(np.int32)
+    pages = (n_past + n_q + 15) // 16
+    nb = int(pages.sum()) + 8
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.zeros((n_sess, int(pages.max())), np.int32)
+    off = 0
+    for i in range(n_sess):
+        tables[i, :pages[i]] = perm[off:off + pages[i]]
+        off += pages[i]
+    L = nova.n_layers
+    per_pool = L * nb * nova.kb * nova.kvw
+    k, v = nova.alloc(per_pool * 2), nova.alloc(per_pool * 2)
+    nova.testkit_fill_normal_f16(k.ptr, per_pool, args.seed + 11, 1.0, s)
+    nova.testkit_fill_normal_f16(v.ptr, per_pool, args.seed + 12, 1.0, s)
+    chunk_elems = n_sess * n_q * nova.kvw
+    kc, vc = nova.alloc(L * chunk_elems * 2), nova.alloc(L * chunk_elems * 2)
+    nova.testkit_fill_normal_f16(kc.ptr, L * chunk_elems, args.seed + 13, 1.0, s)
+    nova.testkit_fill_normal_f16(vc.ptr, L * chunk_elems, args.seed + 14, 1.0, s)
+    q_h = rng.standard_normal((n_sess, n_q, nova.nh, nova.hd)).astype(np.float32)   # one layer's Q
+    q = nova.upload(q_h)
+    o = nova.alloc(L * q_h.nbytes)
+    dt, dp = nova.upload(tables), nova.upload(n_past)
+    stride = tables.shape[1]
+
+    def layer_ops(l):
+        nova.launch_kv_store_paged_batch(k.ptr, v.ptr, dt.ptr, stride, dp.ptr, n_sess, l, nb, n_q,
+                                         kc.ptr + l * chunk_elems * 2, vc.ptr + l * chunk_elems * 2, s)
+        nova.launch_attn_prefill_paged_batch(q.ptr, k.ptr, v.ptr, dt.ptr, stride, dp.ptr, n_sess, n_q, l, nb,
+                                             o.ptr + l * q_h.nbytes, s)
+
+    for l in range(L):
+        layer_ops(l)
+    nova.dev_stream_sync(s)
+    nova.dev_graph_begin(s)
+    for l in range(L):
+        layer_ops(l)
+    g = nova.dev_graph_end(s)
+    for _ in range(args.warmup):
+        nova.dev_graph_launch(g, s)
+    t = Timer(nova, s)
+    t.start()
+    for _ in range(args.steps):
+        nova.dev_graph_launch(g, s)
+    ms = t.stop() / args.steps
+    # attention kernel alone, HIP events around each launch
+    tot = 0.0
+    for l in range(L):
+        t.start()
+        nova.launch_attn_prefill_paged_batch(q.ptr, k.ptr, v.ptr, dt.ptr, stride, dp.ptr, n_sess, n_q, l, nb,
+                                             o.ptr + l * q_h.nbytes, s)
+        tot += t.stop()
+    k_ms = tot / L
+    flops = prefill_flops(n_past, n_q, nova.nh, nova.hd)
+    tflops = flops / (k_ms * 1e-3) / 1e12
+    cpu = None
+    if not args.no_cpu:
+        from oracle_py import Oracle
+        orc = Oracle()
+        shape = (nb, nova.kb, nova.nkv, nova.hd)
+        pk = nova.download(k, shape, np.uint16)          # layer 0 (chunk already appended)
+        pv = nova.download(v, shape, np.uint16)
+        nq_s = 64                                         # bounded sample: first 64 queries of session 0
+        qs = np.ascontiguousarray(q_h[0, :nq_s])
+        t0 = time.perf_counter()
+        ref = orc.attn_prefill_paged("qwen25_7b", qs, pk, pv, np.ascontiguousarray(tables[0]), 0, nb, nq_s,
+                                     int(n_past[0]))
+        secs = time.perf_counter() - t0
+        got = nova.download(o, (n_sess, n_q, nova.nh, nova.hd), np.float32)[0, :nq_s]
+        sample_flops = prefill_flops([n_past[0]], nq_s, nova.nh, nova.hd)
+        cpu = {"value": round(sample_flops / secs / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
+               "sample": f"session 0, first {nq_s} queries, layer 0 (n_past={int(n_past[0])}); C oracle "
+                         f"or_attn_prefill_paged single-threaded, {secs:.2f} s; "
+                         f"max|gpu-cpu| {float(np.abs(got - ref).max()):.2e}"}
+    return {
+        "metric": "chunked-prefill causal paged attention TFLOP/s (config 5, Qwen2.5-7B)",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "us_per_layer": round(ms * 1e3 / L, 2), "higher_is_better": True,
+        "dtype": "f16 MFMA / f32 accumulate", "data": "synthetic (seeded N(0,1) Q/K/V, prefix U[0,4096])",
+        "config": {"workload": "config5: 8 sessions, 512-token chunk appended then causal attention over "
+                               "prefix U[0,4096] + chunk, 28 layers", "n_past": n_past.tolist(), "chunk": n_q},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": load_traffic("prefill"),
+                     "kernel": "prefill_kernel (launch_attn_prefill_paged_batch)",
+                     "kernel_us": round(k_ms * 1e3, 2), "flops_per_launch": flops},
+        "cpu_baseline": cpu,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; multi-GPU figures are not produced "
+                                   "(sessions shard by GPU with no exchange -- see DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    if args.workload == "decode7b":
+        ctx = ragged_ctx(args.seed, 16, 512, 8192)
+        cfg = {"metric": "paged flash-decode KV GB/s (% HBM peak) + us/decode step, Qwen2.5-7B shape",
+               "config": {"workload": "config2: batched ragged paged flash-decode, Qwen2.5-7B attention "
+                                      "(28q/4kv heads, hd128, 28 layers), fp16 KV, 16-token pages, "
+                                      "16 sessions ctx U[512,8192], 1-token append + split-K attention per layer",
+                          "sessions": 16, "ctx": ctx.tolist(), "layers": 28, "page_tokens": 16}}
+        line = run_decode(args, "qwen25_7b", ctx, "decode7b", cfg, "Qwen2.5-7B, 16 sessions")
+    elif args.workload == "longctx14b":
+        ctx = np.full(8, 32767, np.int32)
+        cfg = {"metric": "paged flash-decode KV GB/s, Qwen2.5-14B long context",
+               "config": {"workload": "config4: 8 sessions x 32768 tokens, Qwen2.5-14B attention "
+                                      "(40q/8kv, hd128, 48 layers), ~51.5 GB KV resident",
+                          "sessions": 8, "ctx": 32768, "layers": 48}}
+        line = run_decode(args, "qwen25_14b", ctx, "longctx14b", cfg, "Qwen2.5-14B, 8 x 32K")
+    elif args.workload == "single1p5b":
+        ctx = np.array([1024], np.int32)
+        cfg = {"metric": "paged decode step, Qwen2.5-1.5B single session",
+               "config": {"workload": "config1: 1 session ctx 1024, Qwen2.5-1.5B attention (12q/2kv, 28 layers)",
+                          "sessions": 1, "ctx": 1024, "layers": 28}}
+        line = run_decode(args, "qwen25_1p5b", ctx, "single1p5b", cfg, "Qwen2.5-1.5B, 1 session")
+    elif args.workload == "cow":
+        line = run_cow(args)
+    else:
+        line = run_prefill(args)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

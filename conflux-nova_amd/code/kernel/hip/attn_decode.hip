@@ -6,14 +6,24 @@
 // gathering K/V through the session's block table.  The arithmetic is laid out
 // for CDNA4 instead of the reference's one-warp-per-head scan:
 //
-//  * Work split (stream-K).  The pages of all sessions of a layer form one list
-//    of T pages; workgroup w owns pages [w*T/Gw, (w+1)*T/Gw).  Every workgroup
-//    does the same number of pages whatever the context lengths, so a ragged
-//    batch fills all CUs evenly.  A range that crosses a session boundary
-//    yields one partial (m, l, acc[HD]) per session touched.
-//  * One workgroup = 8 wave64s.  Wave w serves kv head w % NKV and takes every
-//    R-th pair of pages (R = 8/NKV), so the workgroup reads whole 16-token pages
-//    (all kv heads) and each wave streams 256 B rows of its head.
+//  * Work split (session-aligned, balanced).  With T pages in the batch and Gw
+//    target workgroups, session i (P_i pages) gets k_i = ceil(P_i / ceil(T/Gw))
+//    workgroups, each owning a contiguous page range of that session.  Every
+//    workgroup does at most ceil(T/Gw) pages whatever the context lengths, so
+//    a ragged batch fills all CUs evenly, and a workgroup never straddles two
+//    sessions.  Each workgroup writes one partial (m, l, acc[HD]) per head.
+//    Every wave derives the partition itself from one load of n_keys.
+//  * One workgroup = 8 wave64s, one workgroup per CU.  Wave w serves kv head
+//    w % NKV and takes every R-th pair of pages (R = 8/NKV), so the workgroup
+//    reads whole 16-token pages (all kv heads) and each wave streams 256 B rows
+//    of its head; the CU keeps 8 pairs (128 KiB) of K/V outstanding.  The
+//    query operands live once per kv head in LDS.
+//  * Latency hiding inside a wave: the segment's block-table slice is fetched
+//    once (one coalesced load, then v_readlane per page), so no pair waits on
+//    a table lookup.
+//    Page bases are wave-uniform (SGPR) and lane
+//    offsets are fixed 32-bit values, so the loop does no per-lane 64-bit
+//    address arithmetic.
 //  * GQA on the matrix cores.  For a pair of pages (32 keys) a wave forms
 //    S = K . Q^T with v_mfma_f32_16x16x32_f16 (rows = 16 keys of a page, cols =
 //    the G query heads of its kv head padded to 16) and O^T += V^T . P^T with the
@@ -25,19 +35,20 @@
 //    MFMA inputs).  Q (fp32) is split q = hi + lo into two fp16 terms after a
 //    per-head power-of-two scaling, P (fp32 softmax weights) likewise; each
 //    product is two MFMAs accumulating in fp32, leaving ~2^-22 relative error
-//    per operand instead of fp16's 2^-11.
+//    per operand instead of fp16's 2^-11.  The matrix cores have the slack:
+//    the kernel is bound by HBM, not by MFMA issue.
 //  * Online softmax in the log2 domain (exp2f), scale*log2(e) folded into the
 //    per-head factor.  Split partials merge with the reference's combine rule
-//    (max, then l- and acc-weighted sums; rows with l == 0 are skipped).
-//  * Merge: the batched entry point merges in the last workgroup to finish a
-//    session (device-scope counter, self-resetting); the single-session entry
-//    point keeps the reference's scratch contract and uses a combine kernel.
+//    (max, then l- and acc-weighted sums; rows with l == 0 are skipped) in a
+//    second, small kernel: the kernel boundary publishes the partials, so no
+//    workgroup pays for a device-scope fence (an L2 writeback on this part).
 //  * Fused append: the batched entry point can take the layer's new token; the
-//    workgroup that owns the session's last page writes it to the pool and
-//    every lane that needs that row reads it from the input buffer instead, so
-//    no lane ever reads the slot being written.
+//    workgroup that owns the session's last page stores it into the pool and
+//    publishes it to its own waves with a workgroup barrier before any wave
+//    reads that page; no other workgroup reads that page.
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <cstdlib>
 #include <mutex>
 
 #include "check.h"
@@ -55,18 +66,17 @@ constexpr int NH = Model::NH, NKV = Model::NKV, HD = Model::HD, G = Model::G, KV
 constexpr int WAVES = 8;
 constexpr int THREADS = WAVES * 64;
 constexpr int R = WAVES / NKV;           // waves per kv head
-static_assert(WAVES % NKV == 0, "kv heads must divide the 8 waves of a workgroup");
+static_assert(WAVES % NKV == 0, "kv heads must divide the waves of a workgroup");
 constexpr int PW = HD + 2;               // partial row: m, l, acc[HD]
 constexpr int kMaxBatch = 1024;          // sessions per batched launch
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int64_t kPageHalves = (int64_t)kKvBlock * KVW;
+constexpr int64_t kPageBytes = (int64_t)kKvBlock * KVW * 2;
+constexpr int kRowBytes = KVW * 2;
 
 struct DecodeArgs {
     const float* q;          // [n_sess][NH][HD]
     const uint16_t* pool_k;
     const uint16_t* pool_v;
-    uint16_t* wpool_k;       // append targets (== pool_k/pool_v) or null
-    uint16_t* wpool_v;
     const int32_t* tables;
     int64_t table_stride;
     const int32_t* n_keys;   // device [n_sess] or null -> n_keys_scalar
@@ -76,27 +86,91 @@ struct DecodeArgs {
     int nb;
     const uint16_t* k_new;   // [n_sess][NKV][HD] or null
     const uint16_t* v_new;
-    float* o;                // [n_sess][NH][HD]
     float* part;             // [(Gw + n_sess)][NH][PW]
-    int* counters;           // [n_sess], zero between launches
     int gw;                  // workgroups in the grid
 };
 
-__device__ __forceinline__ int owner_of(int64_t page, int64_t T, int gw) {
-    // largest w with floor(w*T/gw) <= page
-    return (int)(((page + 1) * gw - 1) / T);
-}
-
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
-template <bool kInlineMerge>
+__device__ __forceinline__ u4 ld16(const char* base, uint32_t off) {
+    return *reinterpret_cast<const u4*>(base + off);
+}
+
+// The batch partition, derived by one wave from n_keys (every wave that needs
+// it computes it; no LDS, no barrier).  P_i = pages of session i, T = sum P_i,
+// target = ceil(T / gw), k_i = ceil(P_i / target) workgroups for session i,
+// kc_i = k_0 + ... + k_{i-1} its first workgroup (= its first partial slot).
+// Sum k_i <= gw + n_sess, so the grid launches gw + n_sess workgroups.
+struct Part {
+    int sess;      // session of this workgroup, -1 if the workgroup is idle
+    int n_keys;    // keys of that session
+    int pages;     // P_i
+    int k;         // k_i
+    int kc;        // kc_i
+};
+
+__device__ __forceinline__ int nkeys_of(const DecodeArgs& a, int i) {
+    return a.n_keys ? a.n_keys[i] : a.n_keys_scalar;
+}
+
+// Find the session that owns workgroup slot w (find_slot) or the partition
+// entry of session `want` (want >= 0).
+__device__ Part partition(const DecodeArgs& a, int w, int want) {
+    const int lane = threadIdx.x & 63;
+    int T = 0;
+    for (int base = 0; base < a.n_sess; base += 64) {
+        const int i = base + lane;
+        const int nk = i < a.n_sess ? nkeys_of(a, i) : 0;
+        int pg = nk > 0 ? (nk + kKvBlock - 1) >> kKvBlockShift : 0;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) pg += __shfl_xor(pg, o, 64);
+        T += pg;
+    }
+    Part r{-1, 0, 0, 0, 0};
+    if (T == 0) return r;
+    const int target = (T + a.gw - 1) / a.gw;
+    int carry = 0;
+    for (int base = 0; base < a.n_sess; base += 64) {
+        const int i = base + lane;
+        const int nk = i < a.n_sess ? nkeys_of(a, i) : 0;
+        const int pg = nk > 0 ? (nk + kKvBlock - 1) >> kKvBlockShift : 0;
+        const int k = (pg + target - 1) / target;
+        int incl = k;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o, 64);
+            if (lane >= o) incl += t;
+        }
+        const int kc = carry + incl - k;
+        const bool hit = want >= 0 ? (i == want) : (i < a.n_sess && k > 0 && kc <= w && w < kc + k);
+        const uint64_t b = __builtin_amdgcn_ballot_w64(hit);
+        if (b) {
+            const int src = __builtin_ctzll(b);
+            r.sess = base + src;
+            r.n_keys = __shfl(nk, src, 64);
+            r.pages = __shfl(pg, src, 64);
+            r.k = __shfl(k, src, 64);
+            r.kc = __shfl(kc, src, 64);
+            return r;
+        }
+        carry += __shfl(incl, 63, 64);
+    }
+    return r;
+}
+
+// K and V operands of one pair of pages, as loaded
+struct PairRegs {
+    u4 k0[4], k1[4];   // K rows c of page 0 / page 1, halves [32ks + 8g, +8)
+    u4 v[8];           // V rows kappa(g,j) = (page j/4, slot 4g + j%4), halves [8c, +8)
+};
+
 __global__ void __launch_bounds__(THREADS)
-decode_kernel(DecodeArgs a) {
-    __shared__ int s_cu[kMaxBatch + 1];
+decode_split_kernel(DecodeArgs a) {
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];
-    __shared__ float s_acc[WAVES][G][HD];
-    __shared__ int s_flag;
+    __shared__ float s_acc[R > 1 ? WAVES : 1][G][HD];
+    __shared__ u4 s_q[NKV][4][2][64];            // Q^T hi/lo operands per kv head
+    __shared__ float s_qf[NKV][16];              // per-head score factor
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -107,104 +181,97 @@ decode_kernel(DecodeArgs a) {
     const int r = wave / NKV;
     const int w = blockIdx.x;
 
-    // ---- page prefix over sessions (cu[i] = first page of session i) ----
-    const int ns = a.n_sess;
-    if (wave == 0) {
-        int carry = 0;
-        for (int base = 0; base < ns; base += 64) {
-            const int i = base + lane;
-            int nk = 0;
-            if (i < ns) nk = a.n_keys ? a.n_keys[i] : a.n_keys_scalar;
-            int pg = nk > 0 ? (nk + kKvBlock - 1) >> kKvBlockShift : 0;
-            int incl = pg;
+    const Part pt = partition(a, w, -1);
+    if (pt.sess < 0) return;                     // idle workgroup (uniform)
+    const int i = pt.sess;
+    const int n_keys = pt.n_keys;
+    const int j = w - pt.kc;                     // this workgroup's share of session i
+    const int pa = (int)((int64_t)j * pt.pages / pt.k);
+    const int pb = (int)((int64_t)(j + 1) * pt.pages / pt.k);
+    const int last_page = (n_keys - 1) >> kKvBlockShift;
+    const int32_t* table = a.tables + (int64_t)i * a.table_stride;
+
+    // lane-constant byte offsets inside a page
+    const uint32_t koff = (uint32_t)(c * kRowBytes + kvh * HD * 2 + 16 * g);
+    uint32_t voff[4];
 #pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int t = __shfl_up(incl, o, 64);
-                if (lane >= o) incl += t;
+    for (int jj = 0; jj < 4; ++jj) voff[jj] = (uint32_t)((4 * g + jj) * kRowBytes + kvh * HD * 2 + 16 * c);
+
+    const char* pk = reinterpret_cast<const char*>(a.pool_k);
+    const char* pv = reinterpret_cast<const char*>(a.pool_v);
+    const int64_t layer_page0 = (int64_t)a.layer * a.nb;
+
+    {
+        // block-table slice of this workgroup: lane t holds table[pa + 64*chunk + t]
+        int tchunk = 0;
+        int tv = (pa + lane < pb) ? table[pa + lane] : 0;
+        auto phys_of = [&](int pg) -> int {
+            const int rel = pg - pa;
+            if ((rel >> 6) != tchunk) {          // rare: ranges longer than 64 pages
+                tchunk = rel >> 6;
+                const int e = pa + 64 * tchunk + lane;
+                tv = e < pb ? table[e] : 0;
             }
-            if (i < ns) s_cu[i + 1] = carry + incl;
-            carry += __shfl(incl, 63, 64);
-        }
-        if (lane == 0) s_cu[0] = 0;
-    }
-    __syncthreads();
-    const int64_t T = s_cu[ns];
+            return __builtin_amdgcn_readlane(tv, rel & 63);
+        };
 
-    if (kInlineMerge && w == 0) {
-        // sessions without keys produce a zero row (fa_combine: l == 0 -> 0)
-        for (int i = 0; i < ns; ++i)
-            if (s_cu[i + 1] == s_cu[i])
-                for (int idx = tid; idx < NH * HD; idx += THREADS) a.o[(int64_t)i * NH * HD + idx] = 0.f;
-    }
-    if (T == 0) return;
-    // with fewer pages than workgroups, only the first T workgroups take work,
-    // so every participating range is non-empty and owner_of counts arrivals
-    const int gw = a.gw < T ? a.gw : (int)T;
-    if (w >= gw) return;
-    int64_t lo = (int64_t)w * T / gw;
-    const int64_t hi = (int64_t)(w + 1) * T / gw;
-
-    // first session whose pages reach past lo
-    int i = 0;
-    while (s_cu[i + 1] <= lo) ++i;
-
-    while (lo < hi) {
-        const int64_t seg_hi = hi < (int64_t)s_cu[i + 1] ? hi : (int64_t)s_cu[i + 1];
-        const int pa = (int)(lo - s_cu[i]);              // session-local pages [pa, pb)
-        const int pb = (int)(seg_hi - s_cu[i]);
-        const int n_keys = a.n_keys ? a.n_keys[i] : a.n_keys_scalar;
-        const int last_page = (n_keys - 1) >> kKvBlockShift;
-        const int new_slot = (n_keys - 1) & kKvBlockMask;
-        const bool has_new = a.k_new != nullptr;
-        const int32_t* table = a.tables + (int64_t)i * a.table_stride;
-
-        // fused append: the owner of the session's last page stores the new token
-        if (has_new && pb == last_page + 1 && a.wpool_k) {
+        // fused append: the owner of the session's last page stores the new
+        // token; the barrier below publishes it to the waves of this workgroup
+        if (a.k_new && pb == last_page + 1) {
             const int phys = table[last_page];
-            const int64_t dst = ((int64_t)a.layer * a.nb + phys) * kPageHalves + (int64_t)new_slot * KVW;
+            const int64_t dst = ((layer_page0 + phys) * kPageBytes + (int64_t)((n_keys - 1) & kKvBlockMask) * kRowBytes) / 2;
             const int64_t src = (int64_t)i * KVW;
             for (int e = tid; e < KVW / 8; e += THREADS) {
-                *reinterpret_cast<u4*>(a.wpool_k + dst + 8 * e) =
+                *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_k) + dst + 8 * e) =
                     *reinterpret_cast<const u4*>(a.k_new + src + 8 * e);
-                *reinterpret_cast<u4*>(a.wpool_v + dst + 8 * e) =
+                *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_v) + dst + 8 * e) =
                     *reinterpret_cast<const u4*>(a.v_new + src + 8 * e);
             }
         }
 
-        // ---- this wave's query group as split fp16 B operands ----
-        // lane (g,c): head kvh*G + c, dims d = 32*ks + 8*g + j
-        h8 qhi[4], qlo[4];
-        float qf;
-        {
+        // ---- the query group of each kv head as split fp16 B operands, in LDS ----
+        // lane (g,c): head kvh*G + c, dims d = 32*ks + 8*g + j.  The first wave of
+        // each kv head converts; the R waves of that head read them per pair.
+        if (r == 0) {
             float qv[4][8];
             float amax = 0.f;
             const bool real = c < G;
             const float* qp = a.q + ((int64_t)i * NH + kvh * G + (real ? c : 0)) * HD + 8 * g;
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
+            for (int ks = 0; ks < 4; ++ks) {
+                const f4 x0 = *reinterpret_cast<const f4*>(qp + 32 * ks);
+                const f4 x1 = *reinterpret_cast<const f4*>(qp + 32 * ks + 4);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float x = real ? qp[32 * ks + j] : 0.f;
-                    qv[ks][j] = x;
-                    amax = fmaxf(amax, fabsf(x));
+                for (int jj = 0; jj < 4; ++jj) {
+                    qv[ks][jj] = real ? x0[jj] : 0.f;
+                    qv[ks][4 + jj] = real ? x1[jj] : 0.f;
                 }
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) amax = fmaxf(amax, fabsf(qv[ks][jj]));
+            }
             amax = fmaxf(amax, shfl_xor_f(amax, 16));
             amax = fmaxf(amax, shfl_xor_f(amax, 32));
             int ex = 0;
             if (amax > 0.f) (void)frexpf(amax, &ex);
             const int k2 = amax > 0.f ? 15 - ex : 0;    // amax * 2^k2 in [2^14, 2^15)
             const float up = ldexpf(1.f, k2);
-            qf = kScale * kLog2e * ldexpf(1.f, -k2);
+            if (g == 0) s_qf[kvh][c] = kScale * kLog2e * ldexpf(1.f, -k2);
 #pragma unroll
-            for (int ks = 0; ks < 4; ++ks)
+            for (int ks = 0; ks < 4; ++ks) {
+                h8 hi, lo;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float x = qv[ks][j] * up;
+                for (int jj = 0; jj < 8; ++jj) {
+                    const float x = qv[ks][jj] * up;
                     const _Float16 h = (_Float16)x;
-                    qhi[ks][j] = h;
-                    qlo[ks][j] = (_Float16)(x - (float)h);
+                    hi[jj] = h;
+                    lo[jj] = (_Float16)(x - (float)h);
                 }
+                s_q[kvh][ks][0][lane] = __builtin_bit_cast(u4, hi);
+                s_q[kvh][ks][1][lane] = __builtin_bit_cast(u4, lo);
+            }
         }
+        __syncthreads();
+        const float qf = s_qf[kvh][c];
 
         float m = -INFINITY, lsum = 0.f;
         f4 acc[8];
@@ -212,64 +279,64 @@ decode_kernel(DecodeArgs a) {
         for (int cb = 0; cb < 8; ++cb) acc[cb] = f4{0.f, 0.f, 0.f, 0.f};
 
         const int npairs = (pb - pa + 1) >> 1;
-        const int64_t layer_base = (int64_t)a.layer * a.nb;
-        const uint16_t* knew_row = has_new ? a.k_new + (int64_t)i * KVW + kvh * HD : nullptr;
-        const uint16_t* vnew_row = has_new ? a.v_new + (int64_t)i * KVW + kvh * HD : nullptr;
-
-        for (int qp = r; qp < npairs; qp += R) {
+        auto load_pair = [&](int qp, PairRegs& pr) {
             const int pg0 = pa + 2 * qp;
-            const bool two = pg0 + 1 < pb;
-            const int pg1 = two ? pg0 + 1 : pg0;
-            const int phys0 = __builtin_amdgcn_readfirstlane(table[pg0]);
-            const int phys1 = __builtin_amdgcn_readfirstlane(table[pg1]);
-            const uint16_t* kb0 = a.pool_k + (layer_base + phys0) * kPageHalves + kvh * HD;
-            const uint16_t* kb1 = a.pool_k + (layer_base + phys1) * kPageHalves + kvh * HD;
-            const uint16_t* vb0 = a.pool_v + (layer_base + phys0) * kPageHalves + kvh * HD;
-            const uint16_t* vb1 = a.pool_v + (layer_base + phys1) * kPageHalves + kvh * HD;
-
-            // K operand: row c of each page, halves [32ks + 8g, +8)
-            const uint16_t* kr0 = (has_new && pg0 == last_page && c == new_slot) ? knew_row : kb0 + c * KVW;
-            const uint16_t* kr1 = (has_new && pg1 == last_page && c == new_slot) ? knew_row : kb1 + c * KVW;
-            u4 k0[4], k1[4];
+            const int pg1 = pg0 + 1 < pb ? pg0 + 1 : pg0;   // a lone last page loads itself twice
+            const int64_t b0 = (layer_page0 + phys_of(pg0)) * kPageBytes;
+            const int64_t b1 = (layer_page0 + phys_of(pg1)) * kPageBytes;
+            const char* k0 = pk + b0;
+            const char* k1 = pk + b1;
+            const char* v0 = pv + b0;
+            const char* v1 = pv + b1;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                k0[ks] = *reinterpret_cast<const u4*>(kr0 + 32 * ks + 8 * g);
-                k1[ks] = *reinterpret_cast<const u4*>(kr1 + 32 * ks + 8 * g);
+                pr.k0[ks] = ld16(k0, koff + 64 * ks);
+                pr.k1[ks] = ld16(k1, koff + 64 * ks);
             }
-            // V operand: rows kappa(g,j) = page j/4, slot 4g + j%4; halves [8c, 8c+8)
-            u4 vl[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int slot = 4 * g + (j & 3);
-                const int pg = j < 4 ? pg0 : pg1;
-                const uint16_t* vb = j < 4 ? vb0 : vb1;
-                const uint16_t* vr = (has_new && pg == last_page && slot == new_slot) ? vnew_row : vb + slot * KVW;
-                vl[j] = *reinterpret_cast<const u4*>(vr + 8 * c);
+            for (int j = 0; j < 4; ++j) {
+                pr.v[j] = ld16(v0, voff[j]);
+                pr.v[4 + j] = ld16(v1, voff[j]);
             }
+        };
+
+        auto compute_pair = [&](int qp, PairRegs& cur) {
+            const int pg0 = pa + 2 * qp;
+            const bool two = pg0 + 1 < pb;
+            // keys that exist: all of them except in the session's last pair
+            const bool tail = !two || (((pg0 + 2) << kKvBlockShift) > n_keys);
 
             // S = K . Q^T  (C layout: lane (g,c) holds keys 4g+i of head c)
             f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const h8 ka = __builtin_bit_cast(h8, k0[ks]);
-                const h8 kc = __builtin_bit_cast(h8, k1[ks]);
-                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi[ks], s0, 0, 0, 0);
-                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo[ks], s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qhi[ks], s1, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qlo[ks], s1, 0, 0, 0);
+                const h8 ka = __builtin_bit_cast(h8, cur.k0[ks]);
+                const h8 kc = __builtin_bit_cast(h8, cur.k1[ks]);
+                const h8 qhi = __builtin_bit_cast(h8, s_q[kvh][ks][0][lane]);
+                const h8 qlo = __builtin_bit_cast(h8, s_q[kvh][ks][1][lane]);
+                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi, s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qhi, s1, 0, 0, 0);
+                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo, s0, 0, 0, 0);
+                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qlo, s1, 0, 0, 0);
             }
-
-            // mask keys >= n_keys and the missing second page
             float s[8];
             bool ok[8];
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-                const int key0 = (pg0 << kKvBlockShift) + 4 * g + ii;
-                const int key1 = (pg1 << kKvBlockShift) + 4 * g + ii;
-                ok[ii] = key0 < n_keys;
-                ok[4 + ii] = two && key1 < n_keys;
                 s[ii] = s0[ii] * qf;
                 s[4 + ii] = s1[ii] * qf;
+                ok[ii] = true;
+                ok[4 + ii] = true;
+            }
+            if (tail) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    ok[ii] = (pg0 << kKvBlockShift) + 4 * g + ii < n_keys;
+                    ok[4 + ii] = two && ((pg0 + 1) << kKvBlockShift) + 4 * g + ii < n_keys;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (!ok[j]) cur.v[j] = u4{0u, 0u, 0u, 0u};   // unwritten slots may hold NaN bits
             }
             float bm = -INFINITY;
 #pragma unroll
@@ -278,140 +345,178 @@ decode_kernel(DecodeArgs a) {
             bm = fmaxf(bm, shfl_xor_f(bm, 32));
             const float mn = fmaxf(m, bm);
             const float corr = exp2f(m - mn);
-            float p[8];
             float ps = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                p[j] = ok[j] ? exp2f(s[j] - mn) : 0.f;
-                ps += p[j];
-            }
-            lsum = fmaf(lsum, corr, ps);
-            m = mn;
             h8 phi, plo;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const _Float16 h = (_Float16)p[j];
+                const float p = ok[j] ? exp2f(s[j] - mn) : 0.f;
+                ps += p;
+                const _Float16 h = (_Float16)p;
                 phi[j] = h;
-                plo[j] = (_Float16)(p[j] - (float)h);
+                plo[j] = (_Float16)(p - (float)h);
             }
-            // masked V rows are zeroed so garbage (NaN/Inf) in unused slots cannot leak
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                if (!ok[j]) vl[j] = u4{0u, 0u, 0u, 0u};
+            lsum = fmaf(lsum, corr, ps);
+            m = mn;
 
             // O^T += V^T . P^T   (A: lane (g,c) holds V[kappa(g,j)][8c + cb], j = 0..7)
 #pragma unroll
             for (int cb = 0; cb < 8; ++cb) {
-                h8 va;
+                // column cb of the 8 loaded rows: half cb of each 16 B row, paired
+                // into dwords with v_perm (low or high half of dword cb/2)
+                const uint32_t sel = (cb & 1) ? 0x07060302u : 0x05040100u;
+                u4 vw;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) va[j] = __builtin_bit_cast(h8, vl[j])[cb];
+                for (int u = 0; u < 4; ++u)
+                    vw[u] = __builtin_amdgcn_perm(cur.v[2 * u + 1][cb >> 1], cur.v[2 * u][cb >> 1], sel);
+                const h8 va = __builtin_bit_cast(h8, vw);
                 acc[cb] *= corr;
                 acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, phi, acc[cb], 0, 0, 0);
                 acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, plo, acc[cb], 0, 0, 0);
             }
+        };
+
+        // each wave keeps one pair (16 KiB) in flight; the 8 waves of the CU
+        // overlap each other's latency (a register ping-pong of two pairs does
+        // not fit the 256-VGPR budget of 2 waves per SIMD without spilling)
+        for (int qp = r; qp < npairs; qp += R) {
+            PairRegs cur;
+            load_pair(qp, cur);
+            compute_pair(qp, cur);
         }
 
-        // ---- merge the R waves of each kv head in LDS ----
         lsum += shfl_xor_f(lsum, 16);
         lsum += shfl_xor_f(lsum, 32);
-        if (g == 0) {
-            s_m[wave][c] = m;
-            s_l[wave][c] = lsum;
-        }
-        if (c < G) {
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii)
-#pragma unroll
-                for (int cb = 0; cb < 8; ++cb) s_acc[wave][c][8 * (4 * g + ii) + cb] = acc[cb][ii];
-        }
-        __syncthreads();
-
-        // partial slot of (workgroup w, session i): unique because the segment
-        // path is monotone in both w and i
-        float* pout = a.part + (int64_t)(w + i) * NH * PW;
-        for (int idx = tid; idx < NH * HD; idx += THREADS) {
-            const int h = idx / HD, d = idx - h * HD;
-            const int hk = h / G, hc = h - hk * G;
-            float M = -INFINITY;
-#pragma unroll
-            for (int rr = 0; rr < R; ++rr) M = fmaxf(M, s_m[hk + NKV * rr][hc]);
-            float L = 0.f, A = 0.f;
-#pragma unroll
-            for (int rr = 0; rr < R; ++rr) {
-                const int ww = hk + NKV * rr;
-                const float lw = s_l[ww][hc];
-                const float f = lw > 0.f ? exp2f(s_m[ww][hc] - M) : 0.f;
-                L = fmaf(lw, f, L);
-                A = fmaf(s_acc[ww][hc][d], f, A);
-            }
-            pout[(int64_t)h * PW + 2 + d] = A;
-            if (d == 0) {
-                pout[(int64_t)h * PW] = M;
-                pout[(int64_t)h * PW + 1] = L;
-            }
-        }
-
-        if constexpr (kInlineMerge) {
-            const int w_first = owner_of(s_cu[i], T, gw);
-            const int w_last = owner_of((int64_t)s_cu[i + 1] - 1, T, gw);
-            const int nseg = w_last - w_first + 1;
-            __threadfence();
-            __syncthreads();
-            if (tid == 0) {
-                const int old = atomicAdd(a.counters + i, 1);
-                s_flag = (old == nseg - 1);
-            }
-            __syncthreads();
-            if (s_flag) {
-                __threadfence();
-                float* orow = a.o + (int64_t)i * NH * HD;
-                for (int idx = tid; idx < NH * HD; idx += THREADS) {
-                    const int h = idx / HD, d = idx - h * HD;
-                    float M = -INFINITY;
-                    for (int ww = w_first; ww <= w_last; ++ww)
-                        M = fmaxf(M, __builtin_nontemporal_load(a.part + ((int64_t)(ww + i) * NH + h) * PW));
-                    float L = 0.f, A = 0.f;
-                    for (int ww = w_first; ww <= w_last; ++ww) {
-                        const float* pr = a.part + ((int64_t)(ww + i) * NH + h) * PW;
-                        const float ls = __builtin_nontemporal_load(pr + 1);
-                        const float f = ls > 0.f ? exp2f(__builtin_nontemporal_load(pr) - M) : 0.f;
-                        L = fmaf(ls, f, L);
-                        A = fmaf(__builtin_nontemporal_load(pr + 2 + d), f, A);
-                    }
-                    orow[idx] = L > 0.f ? A / L : 0.f;
+        float* pout = a.part + (int64_t)w * NH * PW;
+        if constexpr (R == 1) {
+            // one wave per kv head: its registers are the partial
+            if (c < G) {
+                float* row = pout + (int64_t)(kvh * G + c) * PW;
+                if (g == 0) {
+                    row[0] = m;
+                    row[1] = lsum;
                 }
-                if (tid == 0) a.counters[i] = 0;
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    f4 lo4, hi4;
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) {
+                        lo4[cb] = acc[cb][ii];
+                        hi4[cb] = acc[cb + 4][ii];
+                    }
+                    float* dst = row + 2 + 8 * (4 * g + ii);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        dst[e] = lo4[e];
+                        dst[4 + e] = hi4[e];
+                    }
+                }
+            }
+        } else {
+            // merge the R waves of each kv head in LDS
+            if (g == 0) {
+                s_m[wave][c] = m;
+                s_l[wave][c] = lsum;
+            }
+            if (c < G) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    f4 lo4, hi4;
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) {
+                        lo4[cb] = acc[cb][ii];
+                        hi4[cb] = acc[cb + 4][ii];
+                    }
+                    *reinterpret_cast<f4*>(&s_acc[wave][c][8 * (4 * g + ii)]) = lo4;
+                    *reinterpret_cast<f4*>(&s_acc[wave][c][8 * (4 * g + ii) + 4]) = hi4;
+                }
+            }
+            __syncthreads();
+            for (int idx = tid; idx < NH * HD; idx += THREADS) {
+                const int h = idx / HD, d = idx - h * HD;
+                const int hk = h / G, hc = h - hk * G;
+                float M = -INFINITY;
+#pragma unroll
+                for (int rr = 0; rr < R; ++rr) M = fmaxf(M, s_m[hk + NKV * rr][hc]);
+                float L = 0.f, A = 0.f;
+#pragma unroll
+                for (int rr = 0; rr < R; ++rr) {
+                    const int ww = hk + NKV * rr;
+                    const float lw = s_l[ww][hc];
+                    const float f = lw > 0.f ? exp2f(s_m[ww][hc] - M) : 0.f;
+                    L = fmaf(lw, f, L);
+                    A = fmaf(s_acc[ww][hc][d], f, A);
+                }
+                pout[(int64_t)h * PW + 2 + d] = A;
+                if (d == 0) {
+                    pout[(int64_t)h * PW] = M;
+                    pout[(int64_t)h * PW + 1] = L;
+                }
             }
         }
-        __syncthreads();   // LDS reuse by the next segment
-        lo = seg_hi;
-        ++i;
-        while (i < ns && s_cu[i + 1] == s_cu[i]) ++i;   // skip empty sessions
     }
 }
 
-// Combine for the single-session entry point: nsplit partial rows per head ->
-// O[h][d] (fa_combine_kernel, attn.cu:163-191), partials in the log2 domain.
-__global__ void __launch_bounds__(HD) combine_kernel(const float* __restrict__ part, float* __restrict__ o,
-                                                     int nsplit) {
-    const int h = blockIdx.x, d = threadIdx.x;
-    float M = -INFINITY;
-    for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, part[((int64_t)sp * NH + h) * PW]);
-    float L = 0.f, A = 0.f;
-    for (int sp = 0; sp < nsplit; ++sp) {
-        const float* pr = part + ((int64_t)sp * NH + h) * PW;
-        const float f = pr[1] > 0.f ? exp2f(pr[0] - M) : 0.f;
-        L = fmaf(pr[1], f, L);
-        A = fmaf(pr[2 + d], f, A);
+// Combine: one workgroup per (session, kv head) merges the session's k_i
+// partials (slots kc_i .. kc_i+k_i-1) for the G heads of that kv head with the
+// rule of fa_combine_kernel (attn.cu:163-191): M = max m_s, L = sum over
+// l_s > 0 of l_s*2^(m_s-M), O = sum acc_s*2^(m_s-M) / L; a session without keys
+// gets O = 0.  Thread (hh, q) owns 4 consecutive head-dim columns; the slots
+// are read 16 at a time with all loads in flight, merged online across chunks.
+constexpr int CT = 256;                       // combine threads
+constexpr int kCombineChunk = 16;
+static_assert(G * (HD / 4) <= CT, "combine: one float4 column per thread");
+
+__global__ void __launch_bounds__(CT)
+decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
+    const int i = blockIdx.x, kvh = blockIdx.y;
+    const int tid = threadIdx.x;
+    const Part pt = partition(a, 0, i);
+    const int hh = tid / (HD / 4), q4 = tid - hh * (HD / 4);
+    if (hh >= G) return;
+    f4* orow = reinterpret_cast<f4*>(o + ((int64_t)i * NH + kvh * G + hh) * HD) + q4;
+    if (pt.sess < 0 || pt.k == 0) {
+        *orow = f4{0.f, 0.f, 0.f, 0.f};
+        return;
     }
-    o[h * HD + d] = L > 0.f ? A / L : 0.f;
+    constexpr int64_t SEG = (int64_t)NH * PW;
+    const float* base = a.part + (int64_t)pt.kc * SEG + (int64_t)(kvh * G + hh) * PW;
+    float M = -INFINITY, L = 0.f;
+    f4 A = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < pt.k; s0 += kCombineChunk) {
+        float ms[kCombineChunk], ls[kCombineChunk];
+        f4 as[kCombineChunk];
+#pragma unroll
+        for (int jj = 0; jj < kCombineChunk; ++jj) {
+            const bool in = s0 + jj < pt.k;
+            const float* row = base + (int64_t)(in ? s0 + jj : s0) * SEG;
+            ms[jj] = row[0];
+            ls[jj] = in ? row[1] : 0.f;
+            as[jj] = *reinterpret_cast<const f4*>(row + 2 + 4 * q4);
+        }
+        float mc = M;
+#pragma unroll
+        for (int jj = 0; jj < kCombineChunk; ++jj)
+            if (ls[jj] > 0.f) mc = fmaxf(mc, ms[jj]);
+        const float rescale = L > 0.f ? exp2f(M - mc) : 0.f;
+        L *= rescale;
+        A *= rescale;
+#pragma unroll
+        for (int jj = 0; jj < kCombineChunk; ++jj) {
+            const float f = ls[jj] > 0.f ? exp2f(ms[jj] - mc) : 0.f;
+            L = fmaf(ls[jj], f, L);
+            A += as[jj] * f;
+        }
+        M = mc;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    *orow = A * inv;
 }
 
 int batch_workgroups() {
     static int gw = 0;
     static std::once_flag once;
     std::call_once(once, [] {
-        int per_cu = 2;
+        int per_cu = 1;
         if (const char* e = std::getenv("NOVA_DECODE_WG_PER_CU")) per_cu = std::atoi(e);
         if (per_cu < 1) per_cu = 1;
         int dev = 0, cus = 0;
@@ -422,7 +527,12 @@ int batch_workgroups() {
     return gw;
 }
 
-size_t counters_bytes(int n_sess) { return ((size_t)n_sess * 4 + 255) / 256 * 256; }
+void launch_pair(const DecodeArgs& a, int n_sess, float* o, hipStream_t st) {
+    hipLaunchKernelGGL(decode_split_kernel, dim3(a.gw + n_sess), dim3(THREADS), 0, st, a);
+    NOVA_LAUNCHED();
+    hipLaunchKernelGGL(decode_combine_kernel, dim3(n_sess, NKV), dim3(CT), 0, st, a, o);
+    NOVA_LAUNCHED();
+}
 
 }  // namespace
 }  // namespace nova
@@ -433,7 +543,7 @@ extern "C" {
 
 size_t attn_decode_batch_workspace_bytes(int n_sess) {
     NOVA_REQUIRE(n_sess >= 1 && n_sess <= kMaxBatch);
-    return counters_bytes(n_sess) + (size_t)(batch_workgroups() + n_sess) * NH * PW * sizeof(float);
+    return (size_t)(batch_workgroups() + n_sess) * NH * PW * sizeof(float);
 }
 
 void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* pool_v,
@@ -448,8 +558,6 @@ void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* 
     a.q = q;
     a.pool_k = pool_k;
     a.pool_v = pool_v;
-    a.wpool_k = pool_k;
-    a.wpool_v = pool_v;
     a.tables = tables;
     a.table_stride = table_stride;
     a.n_keys = n_keys;
@@ -458,13 +566,9 @@ void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* 
     a.nb = nb;
     a.k_new = k_new;
     a.v_new = v_new;
-    a.o = o;
-    a.counters = static_cast<int*>(workspace);
-    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + counters_bytes(n_sess));
+    a.part = static_cast<float*>(workspace);
     a.gw = batch_workgroups();
-    hipLaunchKernelGGL(decode_kernel<true>, dim3(a.gw), dim3(THREADS), 0,
-                       reinterpret_cast<hipStream_t>(s), a);
-    NOVA_LAUNCHED();
+    launch_pair(a, n_sess, o, reinterpret_cast<hipStream_t>(s));
 }
 
 void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint16_t* pool_v,
@@ -473,9 +577,10 @@ void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint
     NOVA_REQUIRE(q && pool_k && pool_v && table && o && scratch);
     NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0 && n_keys >= 1);
     const int pages = (n_keys + kKvBlock - 1) >> kKvBlockShift;
-    // scratch holds NH*32*(HD+2) floats (reference contract): at most 32 splits
-    int gw = pages / 2;
-    if (gw > kMaxSplit) gw = kMaxSplit;
+    // scratch holds NH*32*(HD+2) floats (reference contract): at most 32
+    // partial slots, and the partition uses at most gw + 1 of them
+    int gw = (pages + 1) / 2;
+    if (gw > kMaxSplit - 1) gw = kMaxSplit - 1;
     if (gw < 1) gw = 1;
     DecodeArgs a{};
     a.q = q;
@@ -488,14 +593,9 @@ void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint
     a.n_sess = 1;
     a.layer = layer;
     a.nb = nb;
-    a.o = o;
     a.part = scratch;
     a.gw = gw;
-    hipStream_t st = reinterpret_cast<hipStream_t>(s);
-    hipLaunchKernelGGL(decode_kernel<false>, dim3(gw), dim3(THREADS), 0, st, a);
-    NOVA_LAUNCHED();
-    hipLaunchKernelGGL(combine_kernel, dim3(NH), dim3(HD), 0, st, scratch, o, gw);
-    NOVA_LAUNCHED();
+    launch_pair(a, 1, o, reinterpret_cast<hipStream_t>(s));
 }
 
 }  // extern "C"

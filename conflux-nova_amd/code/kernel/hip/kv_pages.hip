@@ -49,6 +49,25 @@ kv_store_kernel(uint16_t* __restrict__ pool_k, uint16_t* __restrict__ pool_v,
     *reinterpret_cast<u4*>(pool_v + dst) = *reinterpret_cast<const u4*>(v + src);
 }
 
+// batched append: session i writes n tokens at positions pos0[i] .. pos0[i]+n-1
+// through tables + i*stride; k/v are [n_sess][n][NKV][HD]
+__global__ void __launch_bounds__(256)
+kv_store_batch_kernel(uint16_t* __restrict__ pool_k, uint16_t* __restrict__ pool_v,
+                      const int32_t* __restrict__ tables, int64_t stride, const int32_t* __restrict__ pos0,
+                      int layer, int nb, int n, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v) {
+    const int sess = blockIdx.y;
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= (int64_t)n * kRowVecs) return;
+    const int t = (int)(e / kRowVecs);
+    const int col = (int)(e - (int64_t)t * kRowVecs);
+    const int64_t pos = (int64_t)pos0[sess] + t;
+    const int phys = tables[sess * stride + (pos >> kKvBlockShift)];
+    const int64_t dst = (((int64_t)layer * nb + phys) * kKvBlock + (pos & kKvBlockMask)) * KVW + 8 * col;
+    const int64_t src = ((int64_t)sess * n + t) * KVW + 8 * col;
+    *reinterpret_cast<u4*>(pool_k + dst) = *reinterpret_cast<const u4*>(k + src);
+    *reinterpret_cast<u4*>(pool_v + dst) = *reinterpret_cast<const u4*>(v + src);
+}
+
 // grid: x = chunks over the 2*L pages of a pair, y = pair index
 __global__ void __launch_bounds__(256)
 cow_copy_kernel(uint16_t* __restrict__ pool_k, uint16_t* __restrict__ pool_v, int nb,
@@ -138,6 +157,20 @@ void launch_kv_store_paged(uint16_t* pool_k, uint16_t* pool_v, const int32_t* ta
     const int64_t vecs = (int64_t)n * kRowVecs;
     hipLaunchKernelGGL(kv_store_kernel, dim3((unsigned)((vecs + 255) / 256)), dim3(256), 0,
                        reinterpret_cast<hipStream_t>(s), pool_k, pool_v, table, layer, nb, n, pos0, k, v);
+    NOVA_LAUNCHED();
+}
+
+void launch_kv_store_paged_batch(uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables, int table_stride,
+                                 const int32_t* pos0, int n_sess, int layer, int nb, int n, const uint16_t* k,
+                                 const uint16_t* v, nova_stream_t s) {
+    NOVA_REQUIRE(pool_k && pool_v && tables && pos0 && k && v);
+    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0 && n >= 0 && n_sess >= 1 && n_sess <= 65535);
+    NOVA_REQUIRE(table_stride > 0);
+    if (n == 0) return;
+    const int64_t vecs = (int64_t)n * kRowVecs;
+    hipLaunchKernelGGL(kv_store_batch_kernel, dim3((unsigned)((vecs + 255) / 256), n_sess), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(s), pool_k, pool_v, tables, (int64_t)table_stride, pos0, layer,
+                       nb, n, k, v);
     NOVA_LAUNCHED();
 }
 

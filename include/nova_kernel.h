@@ -70,9 +70,9 @@ void launch_attn_prefill_paged(const float* q, const uint16_t* pool_k, const uin
  *   k_new, v_new  NULL, or [n_sess][NKV][HD] fp16: the token at position
  *            n_keys[i]-1 is written into the pool AND attended from these
  *            buffers in the same launch (append-then-attend, dense.h:75-95)
- *   workspace    from attn_decode_batch_workspace_bytes(); its 4*n_sess
- *            counter bytes at the start must be zero before the first call
- *            (dev_zero once); every call leaves them zero again.
+ *   workspace    from attn_decode_batch_workspace_bytes(): split partials;
+ *            no initial contents required.
+ * Two launches on s: the split kernel and a small combine kernel.
  * n_keys[i] == 0 yields a zero output row. */
 size_t attn_decode_batch_workspace_bytes(int n_sess);
 void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* pool_v,
@@ -80,6 +80,14 @@ void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* 
                                     int n_sess, int layer, int nb,
                                     const uint16_t* k_new, const uint16_t* v_new,
                                     float* o, void* workspace, nova_stream_t s);
+
+/* Batched append: session i writes n tokens at positions pos0[i]..pos0[i]+n-1
+ * (pos0: device int32[n_sess]) through tables + i*table_stride; k, v:
+ * [n_sess][n][NKV][HD] fp16.  One launch for a decode step's appends (or a
+ * prefill chunk per session) instead of n_sess launch_kv_store_paged calls. */
+void launch_kv_store_paged_batch(uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables, int table_stride,
+                                 const int32_t* pos0, int n_sess, int layer, int nb, int n, const uint16_t* k,
+                                 const uint16_t* v, nova_stream_t s);
 
 /* Batched chunked-prefill attention: n_sess sessions each with a chunk of n_q
  * queries at positions n_past[i]..n_past[i]+n_q-1 (device int32[n_sess]).

@@ -64,14 +64,12 @@ def _batch(nova, fx, q, tables, n_keys, k_new=None, v_new=None):
     dk = nova.upload(k_new) if k_new is not None else None
     dv = nova.upload(v_new) if v_new is not None else None
     outs = []
-    for _ in range(2):   # second call checks the counters were left at zero
+    for _ in range(2):   # a repeated call must give the same bits
         nova.launch_attn_decode_paged_batch(dq.ptr, fx.k.ptr, fx.v.ptr, dt.ptr, tables.shape[1], dn.ptr, n,
                                             LAYER, fx.nb, dk.ptr if dk else None, dv.ptr if dv else None,
                                             do.ptr, ws.ptr, None)
         nova.dev_sync()
         outs.append(do.numpy(q.shape, np.float32))
-    cnt = nova.download(ws, (n,), np.int32)
-    assert (cnt == 0).all(), "merge counters not reset"
     assert np.array_equal(outs[0], outs[1])
     return outs[0]
 

@@ -84,8 +84,9 @@ struct or_pool {
     int n_order;
     int* free_slices;       /* stack, back = next */
     int n_free_slices;
-    int* free_blocks;       /* stack, back = next */
-    int n_free_blocks;
+    int* free_blocks;       /* stack, back = next; grows: freeing an already free
+                               page pushes it again (refcount clamps at 0) */
+    int n_free_blocks, cap_free_blocks;
     int* refcnt;
 };
 
@@ -102,7 +103,8 @@ or_pool* or_pool_new(int n_slices, int64_t ctx) {
     p->nb_total = n_slices * p->nblocks;
     p->refcnt = (int*)calloc((size_t)(p->nb_total > 0 ? p->nb_total : 1), sizeof(int));
     /* free blocks pushed descending => back is the lowest id */
-    p->free_blocks = (int*)malloc(sizeof(int) * (size_t)(p->nb_total + 1));
+    p->cap_free_blocks = p->nb_total + 16;
+    p->free_blocks = (int*)malloc(sizeof(int) * (size_t)p->cap_free_blocks);
     for (int b = p->nb_total - 1; b >= 0; --b) p->free_blocks[p->n_free_blocks++] = b;
     for (int i = 0; i < n_slices; ++i) {
         p->s[i].need_copy_from = -1;
@@ -164,6 +166,10 @@ void or_pool_free_block(or_pool* p, int b) {
     if (b < 0 || b >= p->nb_total) return;
     if (--p->refcnt[b] <= 0) {
         p->refcnt[b] = 0;
+        if (p->n_free_blocks == p->cap_free_blocks) {
+            p->cap_free_blocks *= 2;
+            p->free_blocks = (int*)realloc(p->free_blocks, sizeof(int) * (size_t)p->cap_free_blocks);
+        }
         p->free_blocks[p->n_free_blocks++] = b;
     }
 }

@@ -1,0 +1,81 @@
+"""The C-ABI libraries load on a machine without a GPU and export every entry
+point that include/*.h declares; the Python binding declares the same set."""
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", " ", h.read_text(), flags=re.S)
+        text = re.sub(r"//[^\n]*", " ", text)
+        for m in re.finditer(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\(", text):
+            name = m.group(1)
+            before = text[:m.start()].rstrip()
+            if name in {"if", "for", "while", "sizeof", "return", "defined"} or before.endswith("typedef"):
+                continue
+            # a declaration: preceded by a type token at statement start
+            line = before.split(";")[-1].split("{")[-1].split("}")[-1]
+            if re.search(r"(void|int|float|size_t|uint16_t|uint64_t|int64_t|int32_t|char|nova_\w+_t|nova_geometry)\s*\**\s*$",
+                         line.strip() + " "):
+                names.add(name)
+    return names
+
+
+def test_headers_declare_the_boundary():
+    names = declared_functions()
+    for must in ("dev_alloc", "dev_free", "dev_upload", "dev_download", "dev_sync", "dev_max_alloc",
+                 "launch_kv_store_paged", "launch_attn_decode_paged", "launch_attn_prefill_paged",
+                 "nova_kvpool_cow_slice", "nova_kv_hash_ids", "nova_paged_cow_batch"):
+        assert must in names, must
+
+
+@pytest.mark.parametrize("model", ["qwen25_1p5b", "qwen25_7b", "qwen25_14b"])
+def test_library_exports_every_declared_symbol(model):
+    import nova_amd
+    lib = nova_amd.lib_path(model)
+    assert lib.exists(), f"{lib} not built"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib)], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    missing = sorted(declared_functions() - exported)
+    assert not missing, missing
+
+
+def test_binding_covers_every_declared_symbol():
+    import nova_amd
+    missing = sorted(declared_functions() - set(nova_amd._SIGS))
+    assert not missing, missing
+
+
+def test_library_loads_without_gpu(nova7):
+    # host-only calls work; the device count is simply 0 here
+    assert nova7.nova_model_geometry().nh == 28
+    h = nova7.nova_kvpool_new(2, 64)
+    assert nova7.nova_kvpool_acquire(h) == 0
+    nova7.nova_kvpool_delete(h)
+
+
+def _abort_run(code):
+    return subprocess.run([sys.executable, "-c", code], capture_output=True, text=True,
+                          env={"PYTHONPATH": str(ROOT / "conflux-nova_amd"), "HIP_VISIBLE_DEVICES": ""})
+
+
+@pytest.mark.parametrize("call,needle", [
+    ("n.launch_attn_decode_paged(1, 1, 1, 1, 0, 4, 0, 1, 1, None)", "n_keys >= 1"),
+    ("n.launch_attn_decode_paged(1, 1, 1, 1, 99, 4, 5, 1, 1, None)", "layer < Model::L"),
+    ("n.launch_kv_store_paged(1, 1, 1, 0, 0, 1, 0, 1, 1, None)", "nb > 0"),
+    ("n.launch_attn_prefill_paged(0, 1, 1, 1, 0, 4, 1, 0, 1, None)", "q && pool_k"),
+])
+def test_bad_arguments_abort_before_launch(call, needle):
+    """the reference's abort-only convention (include/nova/config.h:42-63):
+    argument checks fire on the host before anything reaches a device"""
+    r = _abort_run(f"import nova_amd; n = nova_amd.load('qwen25_7b'); {call}")
+    assert r.returncode != 0
+    assert "requirement failed" in r.stderr and needle in r.stderr, r.stderr[-500:]

@@ -47,7 +47,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode7b",
-                    choices=["decode7b", "single1p5b", "cow", "longctx14b", "prefill"])
+                    choices=["decode7b", "single1p5b", "cow", "longctx14b", "prefill", "copycal"])
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
@@ -228,7 +228,7 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
     traffic = load_traffic(workload_name)
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "decode_kernel<true> (launch_attn_decode_paged_batch)",
+            "kernel": "decode_split_kernel + decode_combine_kernel (one launch_attn_decode_paged_batch call)",
             "kernel_us": round(k_ms * 1e3, 2), "bytes_per_launch": bytes_launch}
     cpu = None
     if not args.no_cpu:
@@ -534,6 +534,26 @@ def run_prefill(args):
     }
 
 
+def run_copycal(args):
+    """Plain copy of 1 GiB (testkit_copy): the known-traffic kernel used to
+    calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE (each launch reads and writes
+    exactly 1 GiB)."""
+    nova = nova_amd.load("qwen25_7b")
+    s = nova.dev_stream_create()
+    nbytes = 1 << 30
+    a, b = nova.alloc(nbytes), nova.alloc(nbytes)
+    nova.testkit_fill_normal_f16(a.ptr, nbytes // 2, 1, 1.0, s)
+    for _ in range(args.warmup):
+        nova.testkit_copy(b.ptr, a.ptr, nbytes, s)
+    t = Timer(nova, s)
+    t.start()
+    for _ in range(args.steps):
+        nova.testkit_copy(b.ptr, a.ptr, nbytes, s)
+    ms = t.stop() / args.steps
+    return {"metric": "plain copy GB/s (read + write)", "value": round(2 * nbytes / ms / 1e6, 1), "unit": "GB/s",
+            "bytes_read_per_launch": nbytes, "bytes_written_per_launch": nbytes, "kernel_us": round(ms * 1e3, 2)}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -562,6 +582,8 @@ def main():
                "config": {"workload": "config1: 1 session ctx 1024, Qwen2.5-1.5B attention (12q/2kv, 28 layers)",
                           "sessions": 1, "ctx": 1024, "layers": 28}}
         line = run_decode(args, "qwen25_1p5b", ctx, "single1p5b", cfg, "Qwen2.5-1.5B, 1 session")
+    elif args.workload == "copycal":
+        line = run_copycal(args)
     elif args.workload == "cow":
         line = run_cow(args)
     else:

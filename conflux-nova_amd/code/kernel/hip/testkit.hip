@@ -34,9 +34,29 @@ __global__ void fill_normal_f16_kernel(uint16_t* __restrict__ p, uint64_t n, uin
     }
 }
 
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+__global__ void copy16_kernel(u4* __restrict__ dst, const u4* __restrict__ src, uint64_t n) {
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    for (uint64_t e = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; e < n; e += stride) dst[e] = src[e];
+}
+
 }  // namespace
 
 extern "C" {
+
+// Plain 16-byte-per-lane copy of `bytes` (a multiple of 16): the reference
+// kernel of known traffic that calibrates the HBM byte counters.
+void testkit_copy(void* dst, const void* src, uint64_t bytes, nova_stream_t s) {
+    NOVA_REQUIRE(bytes % 16 == 0);
+    const uint64_t n = bytes / 16;
+    if (n == 0) return;
+    uint64_t blocks = (n + 255) / 256;
+    if (blocks > 16384) blocks = 16384;
+    hipLaunchKernelGGL(copy16_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(s),
+                       static_cast<u4*>(dst), static_cast<const u4*>(src), n);
+    NOVA_LAUNCHED();
+}
 
 // Fill n fp16 values at p with seeded N(0, scale^2) draws.
 void testkit_fill_normal_f16(uint16_t* p, uint64_t n, uint64_t seed, float scale, nova_stream_t s) {

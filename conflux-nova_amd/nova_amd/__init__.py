@@ -77,6 +77,7 @@ _SIGS = {
     "launch_kv_zero_pages": (None, [vp, vp, i32, vp, i32, vp]),
     "launch_table_patch": (None, [vp, vp, vp, i32, vp]),
     "testkit_fill_normal_f16": (None, [vp, u64, u64, f32, vp]),
+    "testkit_copy": (None, [vp, vp, u64, vp]),
     # nova_graph.h
     "nova_kvpool_new": (vp, [i32, i64]),
     "nova_kvpool_delete": (None, [vp]),

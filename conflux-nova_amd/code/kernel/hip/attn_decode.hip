@@ -63,7 +63,10 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
 constexpr int NH = Model::NH, NKV = Model::NKV, HD = Model::HD, G = Model::G, KVW = Model::KVW;
-constexpr int WAVES = 8;
+#ifndef NOVA_DECODE_WAVES
+#define NOVA_DECODE_WAVES 8
+#endif
+constexpr int WAVES = NOVA_DECODE_WAVES;
 constexpr int THREADS = WAVES * 64;
 constexpr int R = WAVES / NKV;           // waves per kv head
 static_assert(WAVES % NKV == 0, "kv heads must divide the waves of a workgroup");
@@ -87,8 +90,21 @@ struct DecodeArgs {
     const uint16_t* k_new;   // [n_sess][NKV][HD] or null
     const uint16_t* v_new;
     float* part;             // [(Gw + n_sess)][NH][PW]
+    const int32_t* plan;     // per-step plan (null: derive the partition in-kernel)
     int gw;                  // workgroups in the grid
 };
+
+// Per-step plan, written once per decode step by decode_plan_kernel (n_keys
+// and block tables are the same for every layer of a step):
+//   session table: n_sess x {kc, k, n_keys, pages}
+//   one record per workgroup slot: {phys[64], sess, pa, pb, n_keys}
+// so a layer's split kernel starts with one load instead of a dependent
+// n_keys -> partition -> block-table chain.
+constexpr int kRecPages = 64;
+constexpr int kRec = kRecPages + 4;
+__host__ __device__ constexpr int64_t plan_ints(int n_sess, int gw) {
+    return (int64_t)n_sess * 4 + (int64_t)(gw + n_sess) * kRec;
+}
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
@@ -181,13 +197,27 @@ decode_split_kernel(DecodeArgs a) {
     const int r = wave / NKV;
     const int w = blockIdx.x;
 
-    const Part pt = partition(a, w, -1);
-    if (pt.sess < 0) return;                     // idle workgroup (uniform)
-    const int i = pt.sess;
-    const int n_keys = pt.n_keys;
-    const int j = w - pt.kc;                     // this workgroup's share of session i
-    const int pa = (int)((int64_t)j * pt.pages / pt.k);
-    const int pb = (int)((int64_t)(j + 1) * pt.pages / pt.k);
+    int i, n_keys, pa, pb, tv;
+    if (a.plan) {
+        // one load: lane t holds phys[t]; lanes 0..3 the header
+        const int32_t* rec = a.plan + (int64_t)a.n_sess * 4 + (int64_t)w * kRec;
+        tv = rec[lane];
+        const int hv = rec[kRecPages + (lane & 3)];
+        i = __builtin_amdgcn_readlane(hv, 0);
+        if (i < 0) return;                       // idle workgroup (uniform)
+        pa = __builtin_amdgcn_readlane(hv, 1);
+        pb = __builtin_amdgcn_readlane(hv, 2);
+        n_keys = __builtin_amdgcn_readlane(hv, 3);
+    } else {
+        const Part pt = partition(a, w, -1);
+        if (pt.sess < 0) return;                 // idle workgroup (uniform)
+        i = pt.sess;
+        n_keys = pt.n_keys;
+        const int j = w - pt.kc;                 // this workgroup's share of session i
+        pa = (int)((int64_t)j * pt.pages / pt.k);
+        pb = (int)((int64_t)(j + 1) * pt.pages / pt.k);
+        tv = (pa + lane < pb) ? a.tables[(int64_t)i * a.table_stride + pa + lane] : 0;
+    }
     const int last_page = (n_keys - 1) >> kKvBlockShift;
     const int32_t* table = a.tables + (int64_t)i * a.table_stride;
 
@@ -204,7 +234,6 @@ decode_split_kernel(DecodeArgs a) {
     {
         // block-table slice of this workgroup: lane t holds table[pa + 64*chunk + t]
         int tchunk = 0;
-        int tv = (pa + lane < pb) ? table[pa + lane] : 0;
         auto phys_of = [&](int pg) -> int {
             const int rel = pg - pa;
             if ((rel >> 6) != tchunk) {          // rare: ranges longer than 64 pages
@@ -215,9 +244,38 @@ decode_split_kernel(DecodeArgs a) {
             return __builtin_amdgcn_readlane(tv, rel & 63);
         };
 
+        const int npairs = (pb - pa + 1) >> 1;
+        auto load_pair = [&](int qp, PairRegs& pr) {
+            const int pg0 = pa + 2 * qp;
+            const int pg1 = pg0 + 1 < pb ? pg0 + 1 : pg0;   // a lone last page loads itself twice
+            const int64_t b0 = (layer_page0 + phys_of(pg0)) * kPageBytes;
+            const int64_t b1 = (layer_page0 + phys_of(pg1)) * kPageBytes;
+            const char* k0 = pk + b0;
+            const char* k1 = pk + b1;
+            const char* v0 = pv + b0;
+            const char* v1 = pv + b1;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                pr.k0[ks] = ld16(k0, koff + 64 * ks);
+                pr.k1[ks] = ld16(k1, koff + 64 * ks);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                pr.v[j] = ld16(v0, voff[j]);
+                pr.v[4 + j] = ld16(v1, voff[j]);
+            }
+        };
+
+        // The first pair's loads go out now, together with the Q loads below,
+        // unless the fused append is about to write into it (then after the barrier).
+        const bool appends = a.k_new && pb == last_page + 1;
+        const bool early = !(appends && pa + 2 * r + 1 >= last_page);
+        PairRegs cur;
+        if (r < npairs && early) load_pair(r, cur);
+
         // fused append: the owner of the session's last page stores the new
         // token; the barrier below publishes it to the waves of this workgroup
-        if (a.k_new && pb == last_page + 1) {
+        if (appends) {
             const int phys = table[last_page];
             const int64_t dst = ((layer_page0 + phys) * kPageBytes + (int64_t)((n_keys - 1) & kKvBlockMask) * kRowBytes) / 2;
             const int64_t src = (int64_t)i * KVW;
@@ -277,28 +335,6 @@ decode_split_kernel(DecodeArgs a) {
         f4 acc[8];
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) acc[cb] = f4{0.f, 0.f, 0.f, 0.f};
-
-        const int npairs = (pb - pa + 1) >> 1;
-        auto load_pair = [&](int qp, PairRegs& pr) {
-            const int pg0 = pa + 2 * qp;
-            const int pg1 = pg0 + 1 < pb ? pg0 + 1 : pg0;   // a lone last page loads itself twice
-            const int64_t b0 = (layer_page0 + phys_of(pg0)) * kPageBytes;
-            const int64_t b1 = (layer_page0 + phys_of(pg1)) * kPageBytes;
-            const char* k0 = pk + b0;
-            const char* k1 = pk + b1;
-            const char* v0 = pv + b0;
-            const char* v1 = pv + b1;
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                pr.k0[ks] = ld16(k0, koff + 64 * ks);
-                pr.k1[ks] = ld16(k1, koff + 64 * ks);
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                pr.v[j] = ld16(v0, voff[j]);
-                pr.v[4 + j] = ld16(v1, voff[j]);
-            }
-        };
 
         auto compute_pair = [&](int qp, PairRegs& cur) {
             const int pg0 = pa + 2 * qp;
@@ -379,8 +415,7 @@ decode_split_kernel(DecodeArgs a) {
         // overlap each other's latency (a register ping-pong of two pairs does
         // not fit the 256-VGPR budget of 2 waves per SIMD without spilling)
         for (int qp = r; qp < npairs; qp += R) {
-            PairRegs cur;
-            load_pair(qp, cur);
+            if (qp != r || !early) load_pair(qp, cur);
             compute_pair(qp, cur);
         }
 
@@ -470,7 +505,17 @@ __global__ void __launch_bounds__(CT)
 decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     const int i = blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x;
-    const Part pt = partition(a, 0, i);
+    Part pt;
+    if (a.plan) {
+        const int32_t* e = a.plan + (int64_t)i * 4;     // {kc, k, n_keys, pages}
+        pt.sess = i;
+        pt.kc = e[0];
+        pt.k = e[1];
+        pt.n_keys = e[2];
+        pt.pages = e[3];
+    } else {
+        pt = partition(a, 0, i);
+    }
     const int hh = tid / (HD / 4), q4 = tid - hh * (HD / 4);
     if (hh >= G) return;
     f4* orow = reinterpret_cast<f4*>(o + ((int64_t)i * NH + kvh * G + hh) * HD) + q4;
@@ -512,6 +557,63 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     *orow = A * inv;
 }
 
+// Per-step plan: block w (< gw + n_sess) writes the record of workgroup slot w;
+// the last block also writes the session table.  64 threads per block.
+__global__ void __launch_bounds__(64)
+decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
+    const int w = blockIdx.x, lane = threadIdx.x;
+    const int n_slots = a.gw + a.n_sess;
+    if (w == n_slots) {
+        // session table: the same prefix as partition(), one lane per session
+        int T = 0;
+        for (int base = 0; base < a.n_sess; base += 64) {
+            const int ii = base + lane;
+            const int nk = ii < a.n_sess ? nkeys_of(a, ii) : 0;
+            int pg = nk > 0 ? (nk + kKvBlock - 1) >> kKvBlockShift : 0;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) pg += __shfl_xor(pg, o, 64);
+            T += pg;
+        }
+        const int target = T > 0 ? (T + a.gw - 1) / a.gw : 1;
+        int carry = 0;
+        for (int base = 0; base < a.n_sess; base += 64) {
+            const int ii = base + lane;
+            const int nk = ii < a.n_sess ? nkeys_of(a, ii) : 0;
+            const int pg = nk > 0 ? (nk + kKvBlock - 1) >> kKvBlockShift : 0;
+            const int k = (pg + target - 1) / target;
+            int incl = k;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(incl, o, 64);
+                if (lane >= o) incl += t;
+            }
+            if (ii < a.n_sess) {
+                int32_t* e = plan + (int64_t)ii * 4;
+                e[0] = carry + incl - k;
+                e[1] = k;
+                e[2] = nk;
+                e[3] = pg;
+            }
+            carry += __shfl(incl, 63, 64);
+        }
+        return;
+    }
+    const Part pt = partition(a, w, -1);
+    int32_t* rec = plan + (int64_t)a.n_sess * 4 + (int64_t)w * kRec;
+    if (pt.sess < 0) {
+        if (lane == 0) rec[kRecPages] = -1;
+        return;
+    }
+    const int j = w - pt.kc;
+    const int pa = (int)((int64_t)j * pt.pages / pt.k);
+    const int pb = (int)((int64_t)(j + 1) * pt.pages / pt.k);
+    rec[lane] = pa + lane < pb ? a.tables[(int64_t)pt.sess * a.table_stride + pa + lane] : 0;
+    if (lane < 4) {
+        const int v = lane == 0 ? pt.sess : lane == 1 ? pa : lane == 2 ? pb : pt.n_keys;
+        rec[kRecPages + lane] = v;
+    }
+}
+
 int batch_workgroups() {
     static int gw = 0;
     static std::once_flag once;
@@ -534,6 +636,23 @@ void launch_pair(const DecodeArgs& a, int n_sess, float* o, hipStream_t st) {
     NOVA_LAUNCHED();
 }
 
+// workspace of the batched path: [plan | partials], each 256-byte aligned
+size_t plan_bytes(int n_sess) { return ((size_t)plan_ints(n_sess, batch_workgroups()) * 4 + 255) / 256 * 256; }
+
+DecodeArgs batch_args(const int32_t* tables, int table_stride, const int32_t* n_keys, int n_sess, void* workspace) {
+    NOVA_REQUIRE(n_sess >= 1 && n_sess <= kMaxBatch);
+    NOVA_REQUIRE(tables && workspace && table_stride > 0);
+    DecodeArgs a{};
+    a.tables = tables;
+    a.table_stride = table_stride;
+    a.n_keys = n_keys;
+    a.n_sess = n_sess;
+    a.gw = batch_workgroups();
+    a.plan = static_cast<const int32_t*>(workspace);
+    a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan_bytes(n_sess));
+    return a;
+}
+
 }  // namespace
 }  // namespace nova
 
@@ -543,32 +662,43 @@ extern "C" {
 
 size_t attn_decode_batch_workspace_bytes(int n_sess) {
     NOVA_REQUIRE(n_sess >= 1 && n_sess <= kMaxBatch);
-    return (size_t)(batch_workgroups() + n_sess) * NH * PW * sizeof(float);
+    return plan_bytes(n_sess) + (size_t)(batch_workgroups() + n_sess) * NH * PW * sizeof(float);
+}
+
+void launch_attn_decode_plan(const int32_t* tables, int table_stride, const int32_t* n_keys, int n_sess,
+                             void* workspace, nova_stream_t s) {
+    NOVA_REQUIRE(n_keys);
+    DecodeArgs a = batch_args(tables, table_stride, n_keys, n_sess, workspace);
+    a.plan = nullptr;   // the plan kernel derives the partition itself
+    hipLaunchKernelGGL(decode_plan_kernel, dim3(a.gw + n_sess + 1), dim3(64), 0, reinterpret_cast<hipStream_t>(s),
+                       a, static_cast<int32_t*>(workspace));
+    NOVA_LAUNCHED();
+}
+
+void launch_attn_decode_paged_planned(const float* q, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
+                                      int table_stride, int n_sess, int layer, int nb, const uint16_t* k_new,
+                                      const uint16_t* v_new, float* o, void* workspace, nova_stream_t s) {
+    NOVA_REQUIRE(q && pool_k && pool_v && o);
+    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0);
+    NOVA_REQUIRE((k_new == nullptr) == (v_new == nullptr));
+    DecodeArgs a = batch_args(tables, table_stride, nullptr, n_sess, workspace);
+    a.q = q;
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.layer = layer;
+    a.nb = nb;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    launch_pair(a, n_sess, o, reinterpret_cast<hipStream_t>(s));
 }
 
 void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* pool_v,
                                     const int32_t* tables, int table_stride, const int32_t* n_keys,
                                     int n_sess, int layer, int nb, const uint16_t* k_new,
                                     const uint16_t* v_new, float* o, void* workspace, nova_stream_t s) {
-    NOVA_REQUIRE(n_sess >= 1 && n_sess <= kMaxBatch);
-    NOVA_REQUIRE(q && pool_k && pool_v && tables && n_keys && o && workspace);
-    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0 && table_stride > 0);
-    NOVA_REQUIRE((k_new == nullptr) == (v_new == nullptr));
-    DecodeArgs a{};
-    a.q = q;
-    a.pool_k = pool_k;
-    a.pool_v = pool_v;
-    a.tables = tables;
-    a.table_stride = table_stride;
-    a.n_keys = n_keys;
-    a.n_sess = n_sess;
-    a.layer = layer;
-    a.nb = nb;
-    a.k_new = k_new;
-    a.v_new = v_new;
-    a.part = static_cast<float*>(workspace);
-    a.gw = batch_workgroups();
-    launch_pair(a, n_sess, o, reinterpret_cast<hipStream_t>(s));
+    launch_attn_decode_plan(tables, table_stride, n_keys, n_sess, workspace, s);
+    launch_attn_decode_paged_planned(q, pool_k, pool_v, tables, table_stride, n_sess, layer, nb, k_new, v_new, o,
+                                     workspace, s);
 }
 
 void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint16_t* pool_v,

@@ -70,11 +70,23 @@ void launch_attn_prefill_paged(const float* q, const uint16_t* pool_k, const uin
  *   k_new, v_new  NULL, or [n_sess][NKV][HD] fp16: the token at position
  *            n_keys[i]-1 is written into the pool AND attended from these
  *            buffers in the same launch (append-then-attend, dense.h:75-95)
- *   workspace    from attn_decode_batch_workspace_bytes(): split partials;
- *            no initial contents required.
- * Two launches on s: the split kernel and a small combine kernel.
+ *   workspace    from attn_decode_batch_workspace_bytes(): plan + split
+ *            partials; no initial contents required.
+ * Three launches on s: plan, split kernel, combine kernel.
  * n_keys[i] == 0 yields a zero output row. */
 size_t attn_decode_batch_workspace_bytes(int n_sess);
+/* The batched call above = launch_attn_decode_plan + launch_attn_decode_paged_planned.
+ * A decode step has the same n_keys and block tables in every layer, so a
+ * caller can plan once per step and run only the planned call per layer:
+ * the plan records each workgroup's session, page range and physical pages,
+ * and the planned call starts from one load instead of a dependent
+ * n_keys -> partition -> block-table chain.  The plan lives at the start of
+ * `workspace`; it is valid until n_keys or the tables change. */
+void launch_attn_decode_plan(const int32_t* tables, int table_stride, const int32_t* n_keys, int n_sess,
+                             void* workspace, nova_stream_t s);
+void launch_attn_decode_paged_planned(const float* q, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
+                                      int table_stride, int n_sess, int layer, int nb, const uint16_t* k_new,
+                                      const uint16_t* v_new, float* o, void* workspace, nova_stream_t s);
 void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* pool_v,
                                     const int32_t* tables, int table_stride, const int32_t* n_keys,
                                     int n_sess, int layer, int nb,

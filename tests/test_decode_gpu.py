@@ -121,3 +121,37 @@ def test_decode_batch_empty_session_and_no_append(nova7, oracle):
             ref = oracle.attn_decode_paged("qwen25_7b", np.ascontiguousarray(q[i]), fx.hk, fx.hv, tables[i],
                                            0, fx.nb, int(n_keys[i]))
             assert_close(got[i], ref)
+
+
+def test_decode_plan_reused_across_layers(nova7, oracle):
+    """one plan per step, planned calls for several layers (bench.py's step)"""
+    nova = nova7
+    n_keys = np.array([700, 33, 1, 2048, 15, 300], np.int32)
+    n = len(n_keys)
+    max_pages = int((n_keys.max() + 15) // 16)
+    nb = n * max_pages + 4
+    rng = np.random.default_rng(12)
+    per_pool = nova.n_layers * nb * nova.kb * nova.kvw
+    k, v = nova.alloc(per_pool * 2), nova.alloc(per_pool * 2)
+    nova.testkit_fill_normal_f16(k.ptr, per_pool, 91, 1.0, None)
+    nova.testkit_fill_normal_f16(v.ptr, per_pool, 92, 1.0, None)
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.ascontiguousarray(perm[: n * max_pages].reshape(n, max_pages))
+    ws = nova.alloc(nova.attn_decode_batch_workspace_bytes(n))
+    dt, dn = nova.upload(tables), nova.upload(n_keys)
+    nova.launch_attn_decode_plan(dt.ptr, max_pages, dn.ptr, n, ws.ptr, None)
+    shape = (nb, nova.kb, nova.nkv, nova.hd)
+    for layer in (0, 7, 27):
+        q = rng.standard_normal((n, nova.nh, nova.hd)).astype(np.float32)
+        dq, do = nova.upload(q), nova.alloc(q.nbytes)
+        nova.launch_attn_decode_paged_planned(dq.ptr, k.ptr, v.ptr, dt.ptr, max_pages, n, layer, nb, None, None,
+                                              do.ptr, ws.ptr, None)
+        nova.dev_sync()
+        got = do.numpy(q.shape, np.float32)
+        off = layer * nb * nova.kb * nova.kvw * 2
+        hk = nova.download(k.ptr + off, shape, np.uint16)
+        hv = nova.download(v.ptr + off, shape, np.uint16)
+        for i in range(n):
+            ref = oracle.attn_decode_paged("qwen25_7b", np.ascontiguousarray(q[i]), hk, hv, tables[i], 0, nb,
+                                           int(n_keys[i]))
+            assert_close(got[i], ref, what=f"layer {layer} session {i}")

@@ -8,23 +8,37 @@
 // streams every key once per query; here the work is a dense contraction:
 //
 //  * Columns.  For one kv head the chunk has n_q*G (query, head) pairs, all
-//    needing the same K/V rows.  A wave owns 4 blocks of 16 such columns
-//    (col = qi*G + hh), a workgroup 4 waves.  Each K/V operand register a wave
-//    loads feeds 4 column blocks.
-//  * Tiles of 32 keys (2 pages).  S^T = K . Q^T (v_mfma_f32_16x16x32_f16, rows =
-//    16 keys of a page, cols = 16 columns), then O^T += V^T . P^T with the same
-//    instruction; S^T's C layout is P^T's B layout (see attn_decode.hip), so
-//    the softmax runs per lane with two cross-lane steps per tile.
-//  * Q is converted to fp16 once (scaled by 1/sqrt(HD)*log2 e); P is fp16; both
-//    accumulate in fp32 (error analysis and the measured error are in the
-//    tests).  kSplitQ switches Q to an exact hi+lo split at 1.5x the MFMA work.
+//    needing the same K/V rows.  A wave owns NB = 2 blocks of 16 such columns
+//    (col = qi*G + hh); a workgroup of 4 waves owns 128 consecutive columns of
+//    one (session, kv head); two workgroups share a CU (2 waves per SIMD, so
+//    one wave's softmax overlaps the other's MFMAs; measured 1.5x over one
+//    wave per SIMD with 4 blocks).
+//  * K/V tiles of 32 keys (2 pages) are staged ONCE per workgroup in LDS,
+//    double-buffered: the global loads of tile t+1 are in flight while tile t
+//    is computed, then written to the other buffer; one barrier per tile.
+//    Rows keep their 256 B but the 16 B chunks are XOR-swizzled by row
+//    (chunk k of row r at position k ^ (r & 15)), so both operand reads below
+//    are free of LDS bank conflicts.
+//  * S^T = K . Q^T with v_mfma_f32_16x16x32_f16 (rows = 16 keys, cols = 16
+//    columns); every K operand read from LDS feeds both column blocks.  S^T's
+//    C layout is the B layout P^T needs, so O^T += V^T . P^T follows without
+//    moving P between lanes; each V operand read feeds both blocks too.
+//  * Q is converted to fp16 once (scaled by 1/sqrt(HD)*log2 e); P is fp16;
+//    accumulation is fp32.  The row sums l come from the matrix core too
+//    (one MFMA of an all-ones operand with P^T per block), so they are the
+//    sums of exactly the fp16 weights applied to V, at no VALU cost.
 //  * Lazy rescaling: a column's running max only moves when a tile's max
 //    exceeds it by more than 8 (log2 units), bounding P by 2^8 in fp16, so the
-//    O rescale (32 multiplies per column block) is skipped on most tiles.
-//  * Causal mask per (key, column); tiles wholly beyond a wave's last query
-//    are never visited.  Workgroups are launched heaviest-first.
+//    O rescale (32 multiplies per block) is skipped on most tiles.
+//  * Softmax statistics cross the four 16-lane rows with v_permlane16/32_swap
+//    (no LDS round trip) and use the raw v_exp_f32; tiles wholly below the
+//    causal diagonal run a mask-free path.
+//  * The block table is read 64 entries at a time into a register and
+//    broadcast with v_readlane; causal masking is per (key, column); tiles past
+//    the workgroup's last query are never visited; heaviest workgroups first.
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <type_traits>
 
 #include "check.h"
 #include "model.h"
@@ -40,13 +54,18 @@ typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 constexpr int NH = Model::NH, NKV = Model::NKV, HD = Model::HD, G = Model::G, KVW = Model::KVW;
 constexpr int WAVES = 4;
 constexpr int THREADS = WAVES * 64;
-constexpr int CB = 4;                          // 16-column blocks per wave
-constexpr int COLS_WAVE = 16 * CB;
+constexpr int NB = 2;                          // 16-column blocks per wave
+constexpr int COLS_WAVE = 16 * NB;
 constexpr int COLS_WG = COLS_WAVE * WAVES;
+constexpr int TILE = 32;                       // keys per stage (2 pages)
+constexpr int ROWB = HD * 2;                   // 256 B per K or V row of one kv head
+constexpr int STAGE_BYTES = 2 * TILE * ROWB;   // K then V
+constexpr int CHUNKS = STAGE_BYTES / 16;       // 16 B chunks per stage
+constexpr int LOADS = CHUNKS / THREADS;        // staging loads per thread per tile
+static_assert(CHUNKS % THREADS == 0, "stage must split evenly over the workgroup");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;                  // rescale threshold, log2 units
-constexpr int64_t kPageHalves = (int64_t)kKvBlock * KVW;
-constexpr bool kSplitQ = false;
+constexpr int64_t kPageBytes = (int64_t)kKvBlock * KVW * 2;
 
 struct PrefillArgs {
     const float* q;            // [n_sess][n_q][NH][HD]
@@ -64,8 +83,33 @@ struct PrefillArgs {
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
-__global__ void __launch_bounds__(THREADS)
+// max / sum over the 4 rows of 16 lanes (lanes c, c+16, c+32, c+48) with the
+// gfx950 row swaps instead of LDS permutes: op(a, b) over the two swap results
+// is the xor-16 (then xor-32) combination for a symmetric op.
+__device__ __forceinline__ float rows_max(float v) {
+    auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
+    auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(y[0]), __uint_as_float(y[1]));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+    auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(x[0]) + __uint_as_float(x[1]);
+    auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(y[0]) + __uint_as_float(y[1]);
+}
+
+// byte offset of (row, chunk) inside a stage half (K or V)
+__device__ __forceinline__ uint32_t swz(int row, int chunk) {
+    return (uint32_t)(row * ROWB + ((chunk ^ (row & 15)) << 4));
+}
+
+// two workgroups per CU (<= 256 registers per wave): while one wave runs its
+// softmax on the VALU the other wave of the SIMD keeps the matrix core busy
+__global__ void __launch_bounds__(THREADS, 2)
 prefill_kernel(PrefillArgs a) {
+    __shared__ __attribute__((aligned(16))) unsigned char s_kv[2][STAGE_BYTES];
+
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
     const int lane = tid & 63;
@@ -81,18 +125,65 @@ prefill_kernel(PrefillArgs a) {
     const float* qs = a.q + (int64_t)sess * a.n_q * NH * HD;
     float* os = a.o + (int64_t)sess * a.n_q * NH * HD;
 
-    const int col0 = cg * COLS_WG + wave * COLS_WAVE;
-    if (col0 >= n_cols) return;
-    const int col_last = min(col0 + COLS_WAVE, n_cols) - 1;
-    const int key_end = n_past + col_last / G + 1;            // exclusive bound for this wave
-    const int key_min_full = n_past + col0 / G + 1;           // keys < this are visible to all columns
+    const int wg_col0 = cg * COLS_WG;
+    const int wg_col_last = min(wg_col0 + COLS_WG, n_cols) - 1;
+    const int key_end = n_past + wg_col_last / G + 1;         // keys the workgroup needs
+    const int n_tiles = (key_end + TILE - 1) / TILE;
+    const int col0 = wg_col0 + wave * COLS_WAVE;
+    const int wave_last = min(col0 + COLS_WAVE, n_cols) - 1;
+    const int wave_key_end = col0 < n_cols ? n_past + wave_last / G + 1 : 0;
+    const int key_min_full = n_past + col0 / G + 1;           // keys below: visible to all columns
+
+    // ---- staging: which 16 B chunks this thread moves for a tile ----
+    // chunk q = tid + THREADS*u: half = q / (TILE*16) (K or V), row = q%512 / 16,
+    // position p = q % 16 holds global chunk p ^ (row & 15).  All lanes of one
+    // load instruction sit in the same page, so the page base is wave-uniform.
+    const char* pk = reinterpret_cast<const char*>(a.pool_k);
+    const char* pv = reinterpret_cast<const char*>(a.pool_v);
+    const int64_t layer_page0 = (int64_t)a.layer * a.nb;
+    int tv = lane < 64 ? 0 : 0;
+    int tchunk = -1;
+    const int n_pages = (key_end + kKvBlock - 1) >> kKvBlockShift;
+    auto phys_of = [&](int pg) -> int {
+        if ((pg >> 6) != tchunk) {
+            tchunk = pg >> 6;
+            const int e = 64 * tchunk + lane;
+            tv = e < n_pages ? table[e] : 0;
+        }
+        return __builtin_amdgcn_readlane(tv, pg & 63);
+    };
+    u4 stg[LOADS];
+    auto load_tile = [&](int t) {
+        const int pg0 = 2 * t;
+        const int pg1 = pg0 + 1 < n_pages ? pg0 + 1 : pg0;   // a lone last page loads itself twice
+        const int64_t b0 = (layer_page0 + phys_of(pg0)) * kPageBytes + kvh * ROWB;
+        const int64_t b1 = (layer_page0 + phys_of(pg1)) * kPageBytes + kvh * ROWB;
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+            const int q = tid + THREADS * u;
+            const int half = q / (TILE * 16);
+            const int row = (q % (TILE * 16)) >> 4;
+            const int p = q & 15;
+            const int chunk = p ^ (row & 15);
+            const char* base = (half ? pv : pk) + ((row >> 4) ? b1 : b0);
+            stg[u] = *reinterpret_cast<const u4*>(base + (int64_t)(row & 15) * (KVW * 2) + 16 * chunk);
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < LOADS; ++u) {
+            const int q = tid + THREADS * u;
+            *reinterpret_cast<u4*>(&s_kv[buf][16 * q]) = stg[u];
+        }
+    };
+
+    if (n_tiles > 0) load_tile(0);
 
     // ---- Q^T operands: lane (g,c) of block b holds column col0 + 16b + c ----
-    h8 qhi[CB][4];
-    h8 qlo[CB][4];
-    int qpos[CB];
+    h8 qh[NB][4];
+    int qpos[NB];
 #pragma unroll
-    for (int b = 0; b < CB; ++b) {
+    for (int b = 0; b < NB; ++b) {
         const int col = col0 + 16 * b + c;
         const bool real = col < n_cols;
         const int qi = real ? col / G : 0;
@@ -100,126 +191,136 @@ prefill_kernel(PrefillArgs a) {
         qpos[b] = real ? n_past + qi : -1;
         const float* qp = qs + ((int64_t)qi * NH + kvh * G + hh) * HD + 8 * g;
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
+        for (int ks = 0; ks < 4; ++ks) {
+            const f4 x0 = *reinterpret_cast<const f4*>(qp + 32 * ks);
+            const f4 x1 = *reinterpret_cast<const f4*>(qp + 32 * ks + 4);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float x = real ? qp[32 * ks + j] * (kScale * kLog2e) : 0.f;
-                const _Float16 h = (_Float16)x;
-                qhi[b][ks][j] = h;
-                qlo[b][ks][j] = (_Float16)(x - (float)h);
+            for (int j = 0; j < 4; ++j) {
+                qh[b][ks][j] = (_Float16)(real ? x0[j] * (kScale * kLog2e) : 0.f);
+                qh[b][ks][4 + j] = (_Float16)(real ? x1[j] * (kScale * kLog2e) : 0.f);
             }
+        }
     }
 
-    float m[CB], lsum[CB];
-    f4 acc[CB][8];
+    float m[NB];
+    f4 lsum[NB];          // row sums from the matrix core: every element = l of column c
+    f4 acc[NB][8];
+    h8 ones;
 #pragma unroll
-    for (int b = 0; b < CB; ++b) {
+    for (int j = 0; j < 8; ++j) ones[j] = (_Float16)1.0f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
         m[b] = -INFINITY;
-        lsum[b] = 0.f;
+        lsum[b] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) acc[b][cb] = f4{0.f, 0.f, 0.f, 0.f};
     }
 
-    const int64_t layer_base = (int64_t)a.layer * a.nb;
-    const int n_tiles = (key_end + 31) >> 5;
+    if (n_tiles > 0) store_tile(0);
+    __syncthreads();
+
     for (int t = 0; t < n_tiles; ++t) {
-        const int pg0 = 2 * t;
-        const bool two = (pg0 + 1) * kKvBlock < key_end;
-        const int pg1 = two ? pg0 + 1 : pg0;
-        const int phys0 = __builtin_amdgcn_readfirstlane(table[pg0]);
-        const int phys1 = __builtin_amdgcn_readfirstlane(table[pg1]);
-        const uint16_t* kb0 = a.pool_k + (layer_base + phys0) * kPageHalves + kvh * HD;
-        const uint16_t* kb1 = a.pool_k + (layer_base + phys1) * kPageHalves + kvh * HD;
-        const uint16_t* vb0 = a.pool_v + (layer_base + phys0) * kPageHalves + kvh * HD;
-        const uint16_t* vb1 = a.pool_v + (layer_base + phys1) * kPageHalves + kvh * HD;
-        u4 k0[4], k1[4], vl[8];
+        if (t + 1 < n_tiles) load_tile(t + 1);
+        const unsigned char* sk = s_kv[t & 1];
+        const unsigned char* sv = sk + TILE * ROWB;
+        const int key_base = t * TILE;
+        // one tile: kMask selects the causal / tail masking (only the tiles
+        // that cross the diagonal or the end of the keys need it)
+        auto tile = [&](auto mask_tag) {
+            constexpr bool kMask = decltype(mask_tag)::value;
+            bool kok[8];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-            k0[ks] = *reinterpret_cast<const u4*>(kb0 + c * KVW + 32 * ks + 8 * g);
-            k1[ks] = *reinterpret_cast<const u4*>(kb1 + c * KVW + 32 * ks + 8 * g);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int slot = 4 * g + (j & 3);
-            vl[j] = *reinterpret_cast<const u4*>((j < 4 ? vb0 : vb1) + slot * KVW + 8 * c);
-        }
-        const int key_base = t * 32;
-        const bool full = key_base + 32 <= key_min_full;       // no causal mask in this tile
-        // keys that exist at all (the tail of the last page may be unwritten)
-        bool kok[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int key = key_base + (j < 4 ? 0 : 16) + 4 * g + (j & 3);
-            kok[j] = key < key_end && (j < 4 || two);
-            if (!kok[j]) vl[j] = u4{0u, 0u, 0u, 0u};
-        }
+            for (int j = 0; j < 8; ++j)
+                kok[j] = !kMask || key_base + (j < 4 ? 0 : 16) + 4 * g + (j & 3) < key_end;
 
-        h8 va[8];
+            // S^T = K . Q^T for both pages and all blocks
+            f4 s0[NB], s1[NB];
 #pragma unroll
-        for (int cb = 0; cb < 8; ++cb)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) va[cb][j] = __builtin_bit_cast(h8, vl[j])[cb];
-
-#pragma unroll
-        for (int b = 0; b < CB; ++b) {
-            f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+            for (int b = 0; b < NB; ++b) {
+                s0[b] = f4{0.f, 0.f, 0.f, 0.f};
+                s1[b] = f4{0.f, 0.f, 0.f, 0.f};
+            }
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, k0[ks]), qhi[b][ks], s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, k1[ks]), qhi[b][ks], s1, 0, 0, 0);
-                if constexpr (kSplitQ) {
-                    s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, k0[ks]), qlo[b][ks], s0, 0, 0, 0);
-                    s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, k1[ks]), qlo[b][ks], s1, 0, 0, 0);
+                const h8 k0 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + swz(c, 4 * ks + g)));
+                const h8 k1 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + swz(16 + c, 4 * ks + g)));
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    s0[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qh[b][ks], s0[b], 0, 0, 0);
+                    s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[b][ks], s1[b], 0, 0, 0);
                 }
             }
-            float s[8];
-            bool ok[8];
-#pragma unroll
-            for (int ii = 0; ii < 4; ++ii) {
-                s[ii] = s0[ii];
-                s[4 + ii] = s1[ii];
-            }
+            // V^T operand rows kappa(g,j) = (page j/4, slot 4g + j%4), chunk c
+            u4 vl[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const int key = key_base + (j < 4 ? 0 : 16) + 4 * g + (j & 3);
-                ok[j] = kok[j] && (full || key <= qpos[b]);
+                const int row = (j < 4 ? 0 : 16) + 4 * g + (j & 3);
+                vl[j] = *reinterpret_cast<const u4*>(sv + swz(row, c));
+                if (kMask && !kok[j]) vl[j] = u4{0u, 0u, 0u, 0u};   // unwritten slots may hold NaN bits
             }
-            float bm = -INFINITY;
+            h8 va[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) bm = ok[j] ? fmaxf(bm, s[j]) : bm;
-            bm = fmaxf(bm, shfl_xor_f(bm, 16));
-            bm = fmaxf(bm, shfl_xor_f(bm, 32));
-            const bool need = bm > m[b] + kLazy;
-            if (__builtin_amdgcn_ballot_w64(need)) {
-                const float mn = need ? bm : m[b];
-                const float corr = exp2f(m[b] - mn);
-                lsum[b] *= corr;
+            for (int cb = 0; cb < 8; ++cb) {
+                const uint32_t sel = (cb & 1) ? 0x07060302u : 0x05040100u;
+                u4 vw;
 #pragma unroll
-                for (int cb = 0; cb < 8; ++cb) acc[b][cb] *= corr;
-                m[b] = mn;
+                for (int uu = 0; uu < 4; ++uu)
+                    vw[uu] = __builtin_amdgcn_perm(vl[2 * uu + 1][cb >> 1], vl[2 * uu][cb >> 1], sel);
+                va[cb] = __builtin_bit_cast(h8, vw);
             }
-            float ps = 0.f;
-            h8 ph;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float p = ok[j] ? exp2f(s[j] - m[b]) : 0.f;
-                const _Float16 hp = (_Float16)p;
-                ph[j] = hp;
-                ps += (float)hp;       // normalise with the weights actually applied
+            for (int b = 0; b < NB; ++b) {
+                float sc[8];
+                bool ok[8];
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    sc[ii] = s0[b][ii];
+                    sc[4 + ii] = s1[b][ii];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int key = key_base + (j < 4 ? 0 : 16) + 4 * g + (j & 3);
+                    ok[j] = !kMask || (kok[j] && key <= qpos[b]);
+                }
+                float bm = -INFINITY;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) bm = ok[j] ? fmaxf(bm, sc[j]) : bm;
+                bm = rows_max(bm);
+                const bool need = bm > m[b] + kLazy;
+                if (__builtin_amdgcn_ballot_w64(need)) {
+                    const float mn = need ? bm : m[b];
+                    const float corr = __builtin_amdgcn_exp2f(m[b] - mn);
+                    lsum[b] *= corr;
+#pragma unroll
+                    for (int cb = 0; cb < 8; ++cb) acc[b][cb] *= corr;
+                    m[b] = mn;
+                }
+                h8 ph;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) ph[j] = (_Float16)(ok[j] ? __builtin_amdgcn_exp2f(sc[j] - m[b]) : 0.f);
+                // l += ones . P^T: the sum of exactly the fp16 weights applied below
+                lsum[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph, lsum[b], 0, 0, 0);
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb)
+                    acc[b][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[cb], ph, acc[b][cb], 0, 0, 0);
             }
-            lsum[b] += ps;
-#pragma unroll
-            for (int cb = 0; cb < 8; ++cb)
-                acc[b][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[cb], ph, acc[b][cb], 0, 0, 0);
+        };
+        if (key_base < wave_key_end) {
+            // a tile needs no mask when every key in it exists and is visible to
+            // every column of the wave
+            if (key_base + TILE <= key_min_full) tile(std::integral_constant<bool, false>{});
+            else tile(std::integral_constant<bool, true>{});
         }
+        if (t + 1 < n_tiles) {
+            store_tile((t + 1) & 1);
+        }
+        __syncthreads();
     }
 
     // ---- normalise and store: lane (g,c) of block b holds d = 8*(4g+i) + cb ----
 #pragma unroll
-    for (int b = 0; b < CB; ++b) {
-        float L = lsum[b];
-        L += shfl_xor_f(L, 16);
-        L += shfl_xor_f(L, 32);
+    for (int b = 0; b < NB; ++b) {
+        const float L = lsum[b][0];
         const int col = col0 + 16 * b + c;
         if (col >= n_cols) continue;
         const int qi = col / G, hh = col - qi * G;

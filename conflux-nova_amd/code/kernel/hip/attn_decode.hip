@@ -8,8 +8,9 @@
 //
 //  * Work split (session-aligned, balanced).  With T pages in the batch and Gw
 //    target workgroups, session i (P_i pages) gets k_i = ceil(P_i / ceil(T/Gw))
-//    workgroups, each owning a contiguous page range of that session.  Every
-//    workgroup does at most ceil(T/Gw) pages whatever the context lengths, so
+//    workgroups (the share is at least 8 pages), each owning a contiguous page
+//    range of that session.  Every workgroup does at most that share whatever
+//    the context lengths, so
 //    a ragged batch fills all CUs evenly, and a workgroup never straddles two
 //    sessions.  Each workgroup writes one partial (m, l, acc[HD]) per head.
 //    Every wave derives the partition itself from one load of n_keys.
@@ -112,9 +113,18 @@ __device__ __forceinline__ u4 ld16(const char* base, uint32_t off) {
     return *reinterpret_cast<const u4*>(base + off);
 }
 
+// Pages per workgroup: the even share ceil(T / gw), but at least kMinShare so
+// that small batches do not spread one or two pages per workgroup (each extra
+// workgroup costs a partial row and a combine term).
+constexpr int kMinShare = 8;
+__host__ __device__ __forceinline__ int share_of(int T, int gw) {
+    const int even = (T + gw - 1) / gw;
+    return even > kMinShare ? even : kMinShare;
+}
+
 // The batch partition, derived by one wave from n_keys (every wave that needs
 // it computes it; no LDS, no barrier).  P_i = pages of session i, T = sum P_i,
-// target = ceil(T / gw), k_i = ceil(P_i / target) workgroups for session i,
+// target = max(ceil(T / gw), 8), k_i = ceil(P_i / target) workgroups for session i,
 // kc_i = k_0 + ... + k_{i-1} its first workgroup (= its first partial slot).
 // Sum k_i <= gw + n_sess, so the grid launches gw + n_sess workgroups.
 struct Part {
@@ -144,7 +154,7 @@ __device__ Part partition(const DecodeArgs& a, int w, int want) {
     }
     Part r{-1, 0, 0, 0, 0};
     if (T == 0) return r;
-    const int target = (T + a.gw - 1) / a.gw;
+    const int target = share_of(T, a.gw);
     int carry = 0;
     for (int base = 0; base < a.n_sess; base += 64) {
         const int i = base + lane;
@@ -574,7 +584,7 @@ decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
             for (int o = 1; o < 64; o <<= 1) pg += __shfl_xor(pg, o, 64);
             T += pg;
         }
-        const int target = T > 0 ? (T + a.gw - 1) / a.gw : 1;
+        const int target = share_of(T, a.gw);
         int carry = 0;
         for (int base = 0; base < a.n_sess; base += 64) {
             const int ii = base + lane;

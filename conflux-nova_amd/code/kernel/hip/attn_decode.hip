@@ -506,9 +506,9 @@ decode_split_kernel(DecodeArgs a) {
 // rule of fa_combine_kernel (attn.cu:163-191): M = max m_s, L = sum over
 // l_s > 0 of l_s*2^(m_s-M), O = sum acc_s*2^(m_s-M) / L; a session without keys
 // gets O = 0.  Thread (hh, q) owns 4 consecutive head-dim columns; the slots
-// are read 16 at a time with all loads in flight, merged online across chunks.
+// are read 32 at a time with all loads in flight, merged online across chunks.
 constexpr int CT = 256;                       // combine threads
-constexpr int kCombineChunk = 16;
+constexpr int kCombineChunk = 32;
 static_assert(G * (HD / 4) <= CT, "combine: one float4 column per thread");
 
 __global__ void __launch_bounds__(CT)

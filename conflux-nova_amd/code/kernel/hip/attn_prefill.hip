@@ -35,7 +35,14 @@
 //    causal diagonal run a mask-free path.
 //  * The block table is read 64 entries at a time into a register and
 //    broadcast with v_readlane; causal masking is per (key, column); tiles past
-//    the workgroup's last query are never visited; heaviest workgroups first.
+//    the workgroup's last query are never visited.
+//  * Scheduling.  A work item is (session, column group); its cost is its
+//    number of key tiles.  Workgroups take items in decreasing cost order
+//    (longest-processing-time first: the dispatcher hands out workgroups in
+//    index order, so the long items start first and the short ones fill the
+//    tail); each workgroup ranks the items itself with an LDS histogram of
+//    the costs.  Kv heads are pinned to XCDs (workgroup w runs on XCD w % 8),
+//    so the column groups that re-read one kv head's K/V share an L2.
 #include <hip/hip_runtime.h>
 #include <cstdint>
 #include <type_traits>
@@ -67,6 +74,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;                  // rescale threshold, log2 units
 constexpr int64_t kPageBytes = (int64_t)kKvBlock * KVW * 2;
 
+static_assert(8 % NKV == 0, "kv heads are pinned to groups of 8 / NKV XCDs");
+constexpr int kXcd = 8;                        // XCDs; workgroup w is dispatched to XCD w % 8
+constexpr int kXcdPerHead = kXcd / NKV;
+constexpr int kBuckets = 4096;                 // cost histogram (tiles; longer items share the top bucket)
+constexpr int kRankMax = 4096;                  // beyond this many items: natural order
+
 struct PrefillArgs {
     const float* q;            // [n_sess][n_q][NH][HD]
     const uint16_t* pool_k;
@@ -75,11 +88,101 @@ struct PrefillArgs {
     int64_t table_stride;
     const int32_t* n_past;     // device [n_sess] or null -> n_past_scalar
     int n_past_scalar;
+    int n_sess;
     int n_q;
     int layer;
     int nb;
     float* o;                  // [n_sess][n_q][NH][HD]
 };
+
+__device__ __forceinline__ int n_past_of(const PrefillArgs& a, int sess) {
+    return a.n_past ? a.n_past[sess] : a.n_past_scalar;
+}
+
+// cost (key tiles) of item j = sess * n_cg + cg, clamped to the histogram
+__device__ __forceinline__ int item_bucket(const PrefillArgs& a, int j, int n_cg, int n_cols) {
+    const int sess = j / n_cg, cg = j - sess * n_cg;
+    const int last_col = min(cg * COLS_WG + COLS_WG, n_cols) - 1;
+    const int key_end = n_past_of(a, sess) + last_col / G + 1;
+    return min((key_end + TILE - 1) / TILE, kBuckets - 1);
+}
+
+// The item of rank r in decreasing cost order (ties in index order).  Every
+// thread of the workgroup calls it (it has barriers) and gets the same answer.
+// s_i: LDS scratch of kBuckets + THREADS + 8 ints.
+__device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int* s_i) {
+    const int N = a.n_sess * n_cg;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int* hist = s_i;
+    int* part = s_i + kBuckets;
+    int* res = part + THREADS;          // [0] group, [1] ranks above it, [2] item, [4..7] wave counts
+    for (int b = tid; b < kBuckets; b += THREADS) hist[b] = 0;
+    __syncthreads();
+    for (int j = tid; j < N; j += THREADS) atomicAdd(&hist[item_bucket(a, j, n_cg, n_cols)], 1);
+    __syncthreads();
+    constexpr int PER = kBuckets / THREADS;
+    int sum = 0;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) sum += hist[PER * tid + u];
+    part[tid] = sum;
+    __syncthreads();
+    if (wave == 0) {
+        // lane l covers groups 4l..4l+3; ranks run from the highest group down
+        int ls = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) ls += part[4 * lane + u];
+        int incl = ls;                                // sum over lanes >= l
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_down(incl, o, 64);
+            if (lane + o < 64) incl += t;
+        }
+        int above = incl - ls;
+#pragma unroll
+        for (int u = 3; u >= 0; --u) {
+            const int gsum = part[4 * lane + u];
+            if (r >= above && r < above + gsum) {
+                res[0] = 4 * lane + u;
+                res[1] = above;
+            }
+            above += gsum;
+        }
+    }
+    __syncthreads();
+    const int grp = res[0];
+    int base = res[1], bucket = PER * grp + PER - 1, o = 0;
+    for (int u = PER - 1; u >= 0; --u) {
+        const int h = hist[PER * grp + u];
+        if (r >= base && r < base + h) {
+            bucket = PER * grp + u;
+            o = r - base;
+        }
+        base += h;
+    }
+    // the o-th item (index order) whose cost falls in that bucket
+    for (int j0 = 0; j0 < N; j0 += THREADS) {
+        const int j = j0 + tid;
+        const bool f = j < N && item_bucket(a, j, n_cg, n_cols) == bucket;
+        const uint64_t bal = __builtin_amdgcn_ballot_w64(f);
+        if (lane == 0) res[4 + wave] = __builtin_popcountll(bal);
+        __syncthreads();
+        int before = 0, total = 0;
+#pragma unroll
+        for (int ww = 0; ww < WAVES; ++ww) {
+            const int n = res[4 + ww];
+            before += ww < wave ? n : 0;
+            total += n;
+        }
+        before += __builtin_popcountll(bal & ((1ull << lane) - 1));
+        if (f && before == o) res[2] = j;
+        __syncthreads();
+        if (o < total) break;
+        o -= total;
+    }
+    const int item = res[2];
+    __syncthreads();                    // the scratch is reused for K/V tiles
+    return item;
+}
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
@@ -109,6 +212,7 @@ __device__ __forceinline__ uint32_t swz(int row, int chunk) {
 __global__ void __launch_bounds__(THREADS, 2)
 prefill_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char s_kv[2][STAGE_BYTES];
+    static_assert((kBuckets + THREADS + 8) * 4 <= (int)sizeof(s_kv), "ranking scratch fits the tile buffers");
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -117,10 +221,18 @@ prefill_kernel(PrefillArgs a) {
     const int c = lane & 15;
     const int n_cols = a.n_q * G;
     const int n_cg = (n_cols + COLS_WG - 1) / COLS_WG;
-    const int cg = n_cg - 1 - (int)blockIdx.x;           // heaviest (latest queries) first
-    const int kvh = blockIdx.y;
-    const int sess = blockIdx.z;
-    const int n_past = a.n_past ? a.n_past[sess] : a.n_past_scalar;
+    const int N = a.n_sess * n_cg;
+    // workgroup -> (kv head, rank): kv head h runs on XCDs [h*kXcdPerHead, +kXcdPerHead)
+    const int xcd = (int)blockIdx.x % kXcd;
+    const int kvh = xcd / kXcdPerHead;
+    const int rank = ((int)blockIdx.x / kXcd) * kXcdPerHead + xcd % kXcdPerHead;
+    if (rank >= N) return;                                  // grid padding (uniform)
+    int item;
+    if (a.n_sess == 1 || N > kRankMax) item = (rank / n_cg) * n_cg + (n_cg - 1 - rank % n_cg);
+    else item = lpt_item(a, rank, n_cg, n_cols, reinterpret_cast<int*>(&s_kv[0][0]));
+    const int sess = item / n_cg;
+    const int cg = item - sess * n_cg;
+    const int n_past = n_past_of(a, sess);
     const int32_t* table = a.tables + (int64_t)sess * a.table_stride;
     const float* qs = a.q + (int64_t)sess * a.n_q * NH * HD;
     float* os = a.o + (int64_t)sess * a.n_q * NH * HD;
@@ -341,8 +453,10 @@ prefill_kernel(PrefillArgs a) {
 }
 
 void launch(const PrefillArgs& a, int n_sess, hipStream_t s) {
-    const int n_cg = (a.n_q * G + COLS_WG - 1) / COLS_WG;
-    hipLaunchKernelGGL(prefill_kernel, dim3(n_cg, NKV, n_sess), dim3(THREADS), 0, s, a);
+    const int64_t n_cg = (a.n_q * G + COLS_WG - 1) / COLS_WG;
+    const int64_t n_wg = (n_cg * n_sess * NKV + kXcd - 1) / kXcd * kXcd;
+    NOVA_REQUIRE(n_wg < (int64_t)1 << 31);
+    hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)n_wg), dim3(THREADS), 0, s, a);
     NOVA_LAUNCHED();
 }
 
@@ -367,6 +481,7 @@ void launch_attn_prefill_paged(const float* q, const uint16_t* pool_k, const uin
     a.table_stride = 0;
     a.n_past = nullptr;
     a.n_past_scalar = n_past;
+    a.n_sess = 1;
     a.n_q = n_q;
     a.layer = layer;
     a.nb = nb;
@@ -388,6 +503,7 @@ void launch_attn_prefill_paged_batch(const float* q, const uint16_t* pool_k, con
     a.tables = tables;
     a.table_stride = table_stride;
     a.n_past = n_past;
+    a.n_sess = n_sess;
     a.n_q = n_q;
     a.layer = layer;
     a.nb = nb;

@@ -79,3 +79,32 @@ def test_prefill_batch_matches_single(nova7, oracle):
         ref = oracle.attn_prefill_paged("qwen25_7b", np.ascontiguousarray(q[i]), fx.hk, fx.hv, tables[i], 0, fx.nb,
                                         n_q, int(n_past[i]))
         assert_close(got[i], ref, what=f"session {i}")
+
+
+@pytest.mark.parametrize("model,n_q,n_past", [
+    ("qwen25_7b", 100, [0, 600, 600, 37, 255, 600]),      # ties, 6 sessions x 6 column groups
+    ("qwen25_1p5b", 45, [300, 0, 17]),                    # NKV=2: 3 items per kv head, padded grid
+    ("qwen25_14b", 70, [5, 129, 64, 64, 400]),            # NKV=8
+])
+def test_prefill_batch_ranked_order(model, n_q, n_past, oracle):
+    """Many (session, column group) items taken in decreasing cost order: every
+    output row is written exactly by its own item (the output starts as NaN)."""
+    import nova_amd
+    nova = nova_amd.load(model)
+    n_past = np.array(n_past, np.int32)
+    n = len(n_past)
+    print(f"[case] prefill batch model={model} n_q={n_q} n_past={n_past.tolist()}", flush=True)
+    pages = int((n_past.max() + n_q + 15) // 16)
+    fx = PagedFixture(nova, nb=n * pages + 2, layer=LAYER, seed=int(n_past.sum()) + n_q)
+    tables = fx.tables(n, pages)
+    q = fx.rng.standard_normal((n, n_q, nova.nh, nova.hd)).astype(np.float32)
+    dq, dt, dn = nova.upload(q), nova.upload(tables), nova.upload(n_past)
+    do = nova.upload(np.full(q.shape, np.nan, np.float32))
+    nova.launch_attn_prefill_paged_batch(dq.ptr, fx.k.ptr, fx.v.ptr, dt.ptr, pages, dn.ptr, n, n_q, LAYER, fx.nb,
+                                         do.ptr, None)
+    nova.dev_sync()
+    got = do.numpy(q.shape, np.float32)
+    for i in range(n):
+        ref = oracle.attn_prefill_paged(model, np.ascontiguousarray(q[i]), fx.hk, fx.hv, tables[i], 0, fx.nb,
+                                        n_q, int(n_past[i]))
+        assert_close(got[i], ref, what=f"{model} session {i}")

@@ -22,7 +22,14 @@
 //  * S^T = K . Q^T with v_mfma_f32_16x16x32_f16 (rows = 16 keys, cols = 16
 //    columns); every K operand read from LDS feeds both column blocks.  S^T's
 //    C layout is the B layout P^T needs, so O^T += V^T . P^T follows without
-//    moving P between lanes; each V operand read feeds both blocks too.
+//    moving P between lanes; each V operand read feeds both blocks too.  The
+//    V^T operand (8 keys of one d per lane) comes straight out of LDS with the
+//    gfx950 transposing read ds_read_b64_tr_b16: within each 16-lane group,
+//    lane i's element j is element (i & 3) of what lane 4j + (i >> 2) points
+//    at, so lane s of group g points at key row 4g + (s >> 2), halfs
+//    d0 + 4 (s & 3) .. +3, and receives V[4g + j][d0 + s], j = 0..3.
+//  * Rows past the workgroup's last key (unwritten slots may hold NaN bits)
+//    are staged as zeros, so masked weights never meet NaN operands.
 //  * Q is converted to fp16 once (scaled by 1/sqrt(HD)*log2 e); P is fp16;
 //    accumulation is fp32.  The row sums l come from the matrix core too
 //    (one MFMA of an all-ones operand with P^T per block), so they are the
@@ -57,6 +64,9 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef __fp16 tr4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef __attribute__((address_space(3))) tr4 lds_tr4;
 
 constexpr int NH = Model::NH, NKV = Model::NKV, HD = Model::HD, G = Model::G, KVW = Model::KVW;
 constexpr int WAVES = 4;
@@ -202,6 +212,12 @@ __device__ __forceinline__ float rows_sum(float v) {
     return __uint_as_float(y[0]) + __uint_as_float(y[1]);
 }
 
+// 4 halfs of a 16-bit matrix, transposed across each group of 16 lanes
+__device__ __forceinline__ u2 lds_read_tr(const unsigned char* p) {
+    const auto lp = (lds_tr4*)(__attribute__((address_space(3))) unsigned char*)p;
+    return __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(lp));
+}
+
 // byte offset of (row, chunk) inside a stage half (K or V)
 __device__ __forceinline__ uint32_t swz(int row, int chunk) {
     return (uint32_t)(row * ROWB + ((chunk ^ (row & 15)) << 4));
@@ -280,6 +296,13 @@ prefill_kernel(PrefillArgs a) {
             const char* base = (half ? pv : pk) + ((row >> 4) ? b1 : b0);
             stg[u] = *reinterpret_cast<const u4*>(base + (int64_t)(row & 15) * (KVW * 2) + 16 * chunk);
         }
+        if (TILE * (t + 1) > key_end) {                      // the tile holding the last key
+#pragma unroll
+            for (int u = 0; u < LOADS; ++u) {
+                const int row = ((tid + THREADS * u) % (TILE * 16)) >> 4;
+                if (TILE * t + row >= key_end) stg[u] = u4{0u, 0u, 0u, 0u};
+            }
+        }
     };
     auto store_tile = [&](int buf) {
 #pragma unroll
@@ -328,6 +351,16 @@ prefill_kernel(PrefillArgs a) {
         for (int cb = 0; cb < 8; ++cb) acc[b][cb] = f4{0.f, 0.f, 0.f, 0.f};
     }
 
+    // V^T operand addresses: lane s of group g reads key row 4g + (s >> 2) (and
+    // +16, the second page), halfs 16cb + 4 (s & 3) .. +3 of it
+    uint32_t voff[8];
+    {
+        const int vr = 4 * g + (c >> 2);
+        const int vh = (c >> 1) & 1;
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) voff[cb] = swz(vr, 2 * cb + vh) + 8 * (c & 1);
+    }
+
     if (n_tiles > 0) store_tile(0);
     __syncthreads();
 
@@ -340,10 +373,6 @@ prefill_kernel(PrefillArgs a) {
         // that cross the diagonal or the end of the keys need it)
         auto tile = [&](auto mask_tag) {
             constexpr bool kMask = decltype(mask_tag)::value;
-            bool kok[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                kok[j] = !kMask || key_base + (j < 4 ? 0 : 16) + 4 * g + (j & 3) < key_end;
 
             // S^T = K . Q^T for both pages and all blocks
             f4 s0[NB], s1[NB];
@@ -362,23 +391,14 @@ prefill_kernel(PrefillArgs a) {
                     s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[b][ks], s1[b], 0, 0, 0);
                 }
             }
-            // V^T operand rows kappa(g,j) = (page j/4, slot 4g + j%4), chunk c
-            u4 vl[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int row = (j < 4 ? 0 : 16) + 4 * g + (j & 3);
-                vl[j] = *reinterpret_cast<const u4*>(sv + swz(row, c));
-                if (kMask && !kok[j]) vl[j] = u4{0u, 0u, 0u, 0u};   // unwritten slots may hold NaN bits
-            }
+            // V^T operands: va[cb] row c = d 16cb + c, k = keys kappa(g, j) =
+            // (page j / 4, slot 4g + j % 4), the k order of P^T below
             h8 va[8];
 #pragma unroll
             for (int cb = 0; cb < 8; ++cb) {
-                const uint32_t sel = (cb & 1) ? 0x07060302u : 0x05040100u;
-                u4 vw;
-#pragma unroll
-                for (int uu = 0; uu < 4; ++uu)
-                    vw[uu] = __builtin_amdgcn_perm(vl[2 * uu + 1][cb >> 1], vl[2 * uu][cb >> 1], sel);
-                va[cb] = __builtin_bit_cast(h8, vw);
+                const u2 lo = lds_read_tr(sv + voff[cb]);
+                const u2 hi = lds_read_tr(sv + voff[cb] + 16 * ROWB);
+                va[cb] = __builtin_bit_cast(h8, u4{lo[0], lo[1], hi[0], hi[1]});
             }
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
@@ -392,7 +412,7 @@ prefill_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int key = key_base + (j < 4 ? 0 : 16) + 4 * g + (j & 3);
-                    ok[j] = !kMask || (kok[j] && key <= qpos[b]);
+                    ok[j] = !kMask || key <= qpos[b];
                 }
                 float bm = -INFINITY;
 #pragma unroll
@@ -429,7 +449,7 @@ prefill_kernel(PrefillArgs a) {
         __syncthreads();
     }
 
-    // ---- normalise and store: lane (g,c) of block b holds d = 8*(4g+i) + cb ----
+    // ---- normalise and store: lane (g,c) of block b holds d = 16cb + 4g + i ----
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const float L = lsum[b][0];
@@ -439,16 +459,7 @@ prefill_kernel(PrefillArgs a) {
         float* op = os + ((int64_t)qi * NH + kvh * G + hh) * HD;
         const float inv = 1.f / L;
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-            f4 lo4, hi4;
-#pragma unroll
-            for (int cb = 0; cb < 4; ++cb) {
-                lo4[cb] = acc[b][cb][ii] * inv;
-                hi4[cb] = acc[b][cb + 4][ii] * inv;
-            }
-            *reinterpret_cast<f4*>(op + 8 * (4 * g + ii)) = lo4;
-            *reinterpret_cast<f4*>(op + 8 * (4 * g + ii) + 4) = hi4;
-        }
+        for (int cb = 0; cb < 8; ++cb) *reinterpret_cast<f4*>(op + 16 * cb + 4 * g) = acc[b][cb] * inv;
     }
 }
 

@@ -13,9 +13,10 @@
 //    one (session, kv head); two workgroups share a CU (2 waves per SIMD, so
 //    one wave's softmax overlaps the other's MFMAs; measured 1.5x over one
 //    wave per SIMD with 4 blocks).
-//  * K/V tiles of 32 keys (2 pages) are staged ONCE per workgroup in LDS,
-//    double-buffered: the global loads of tile t+1 are in flight while tile t
-//    is computed, then written to the other buffer; one barrier per tile.
+//  * K/V tiles of 32 keys (2 pages) are staged ONCE per workgroup in LDS by
+//    direct global->LDS loads (global_load_lds_dwordx4: no staging
+//    registers), NBUF buffers deep: tiles t+1 .. t+NBUF-1 are in flight while
+//    tile t is computed; one barrier per tile.
 //    Rows keep their 256 B but the 16 B chunks are XOR-swizzled by row
 //    (chunk k of row r at position k ^ (r & 15)), so both operand reads below
 //    are free of LDS bank conflicts.
@@ -29,7 +30,8 @@
 //    at, so lane s of group g points at key row 4g + (s >> 2), halfs
 //    d0 + 4 (s & 3) .. +3, and receives V[4g + j][d0 + s], j = 0..3.
 //  * Rows past the workgroup's last key (unwritten slots may hold NaN bits)
-//    are staged as zeros, so masked weights never meet NaN operands.
+//    are loaded from a zero row instead, so masked weights never meet NaN
+//    operands.
 //  * Q is converted to fp16 once (scaled by 1/sqrt(HD)*log2 e); P is fp16;
 //    accumulation is fp32.  The row sums l come from the matrix core too
 //    (one MFMA of an all-ones operand with P^T per block), so they are the
@@ -40,9 +42,10 @@
 //  * Softmax statistics cross the four 16-lane rows with v_permlane16/32_swap
 //    (no LDS round trip) and use the raw v_exp_f32; tiles wholly below the
 //    causal diagonal run a mask-free path.
-//  * The block table is read 64 entries at a time into a register and
-//    broadcast with v_readlane; causal masking is per (key, column); tiles past
-//    the workgroup's last query are never visited.
+//  * The workgroup's slice of the block table sits in LDS (windows of 4096
+//    pages), so a page lookup never waits on the vector-memory counter that
+//    the tile loads in flight occupy; causal masking is per (key, column);
+//    tiles past the workgroup's last query are never visited.
 //  * Scheduling.  A work item is (session, column group); its cost is its
 //    number of key tiles.  Workgroups take items in decreasing cost order
 //    (longest-processing-time first: the dispatcher hands out workgroups in
@@ -69,6 +72,11 @@ typedef __fp16 tr4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) tr4 lds_tr4;
 
 constexpr int NH = Model::NH, NKV = Model::NKV, HD = Model::HD, G = Model::G, KVW = Model::KVW;
+#ifndef NOVA_PREFILL_NBUF
+#define NOVA_PREFILL_NBUF 3
+#endif
+constexpr int NBUF = NOVA_PREFILL_NBUF;        // K/V tile buffers in LDS
+static_assert(NBUF == 2 || NBUF == 3, "two or three tile buffers");
 constexpr int WAVES = 4;
 constexpr int THREADS = WAVES * 64;
 constexpr int NB = 2;                          // 16-column blocks per wave
@@ -89,6 +97,7 @@ constexpr int kXcd = 8;                        // XCDs; workgroup w is dispatche
 constexpr int kXcdPerHead = kXcd / NKV;
 constexpr int kBuckets = 4096;                 // cost histogram (tiles; longer items share the top bucket)
 constexpr int kRankMax = 4096;                  // beyond this many items: natural order
+constexpr int kTabWin = 4096;                   // block-table entries held in LDS
 
 struct PrefillArgs {
     const float* q;            // [n_sess][n_q][NH][HD]
@@ -196,6 +205,34 @@ __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int* 
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
+// 16 zero bytes in global memory: the source of the tail rows' loads
+__device__ __attribute__((aligned(16))) u4 g_zero16;
+
+// direct 16 B per lane global -> LDS load; the wave writes 1 KiB at lds (uniform).
+// Issued as inline asm so that the compiler's own vmcnt bookkeeping does not
+// see it: the builtin makes the compiler drain every pending load (including
+// the tiles still meant to be in flight) before each LDS read it cannot prove
+// disjoint.  The pipeline waits for these loads explicitly (tile_barrier);
+// the compiler's waits for its own loads stay correct, as the counter drains
+// in issue order.
+__device__ __forceinline__ void dma16(const void* src, unsigned char* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+}
+
+// workgroup barrier for the tile pipeline: the wave's own direct loads of the
+// next tile are complete (vmcnt <= pending, the later tiles may stay in
+// flight), then s_barrier; the empty asm statements keep the compiler from
+// moving LDS accesses across it
+template <int kPending>
+__device__ __forceinline__ void tile_barrier() {
+    if constexpr (kPending == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kPending) : "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // max / sum over the 4 rows of 16 lanes (lanes c, c+16, c+32, c+48) with the
 // gfx950 row swaps instead of LDS permutes: op(a, b) over the two swap results
 // is the xor-16 (then xor-32) combination for a symmetric op.
@@ -227,7 +264,8 @@ __device__ __forceinline__ uint32_t swz(int row, int chunk) {
 // softmax on the VALU the other wave of the SIMD keeps the matrix core busy
 __global__ void __launch_bounds__(THREADS, 2)
 prefill_kernel(PrefillArgs a) {
-    __shared__ __attribute__((aligned(16))) unsigned char s_kv[2][STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) unsigned char s_kv[NBUF][STAGE_BYTES];
+    __shared__ int32_t s_tab[kTabWin];
     static_assert((kBuckets + THREADS + 8) * 4 <= (int)sizeof(s_kv), "ranking scratch fits the tile buffers");
 
     const int tid = threadIdx.x;
@@ -269,50 +307,44 @@ prefill_kernel(PrefillArgs a) {
     const char* pk = reinterpret_cast<const char*>(a.pool_k);
     const char* pv = reinterpret_cast<const char*>(a.pool_v);
     const int64_t layer_page0 = (int64_t)a.layer * a.nb;
-    int tv = lane < 64 ? 0 : 0;
-    int tchunk = -1;
     const int n_pages = (key_end + kKvBlock - 1) >> kKvBlockShift;
-    auto phys_of = [&](int pg) -> int {
-        if ((pg >> 6) != tchunk) {
-            tchunk = pg >> 6;
-            const int e = 64 * tchunk + lane;
-            tv = e < n_pages ? table[e] : 0;
-        }
-        return __builtin_amdgcn_readlane(tv, pg & 63);
+    int win0 = 0;                                            // first page of the LDS table window
+    auto load_window = [&](int first) {                      // every thread, uniform
+        for (int e = tid; e < kTabWin && first + e < n_pages; e += THREADS) s_tab[e] = table[first + e];
+        __syncthreads();
+        win0 = first;
     };
-    u4 stg[LOADS];
-    auto load_tile = [&](int t) {
+    load_window(0);
+    // physical page of logical page pg; the window only moves forward, one
+    // tile at a time, and all waves move it together (between two barriers)
+    auto phys_of = [&](int pg) -> int {
+        if (pg - win0 >= kTabWin) {
+            __syncthreads();                                 // every wave is done with the old window
+            load_window(pg);
+        }
+        return s_tab[pg - win0];
+    };
+    auto load_tile = [&](int t, int buf) {
         const int pg0 = 2 * t;
         const int pg1 = pg0 + 1 < n_pages ? pg0 + 1 : pg0;   // a lone last page loads itself twice
         const int64_t b0 = (layer_page0 + phys_of(pg0)) * kPageBytes + kvh * ROWB;
         const int64_t b1 = (layer_page0 + phys_of(pg1)) * kPageBytes + kvh * ROWB;
+        const bool tail = TILE * (t + 1) > key_end;         // the tile holding the last key
 #pragma unroll
         for (int u = 0; u < LOADS; ++u) {
-            const int q = tid + THREADS * u;
+            const int q = tid + THREADS * u;                 // LDS chunk q of the stage
             const int half = q / (TILE * 16);
             const int row = (q % (TILE * 16)) >> 4;
             const int p = q & 15;
             const int chunk = p ^ (row & 15);
-            const char* base = (half ? pv : pk) + ((row >> 4) ? b1 : b0);
-            stg[u] = *reinterpret_cast<const u4*>(base + (int64_t)(row & 15) * (KVW * 2) + 16 * chunk);
-        }
-        if (TILE * (t + 1) > key_end) {                      // the tile holding the last key
-#pragma unroll
-            for (int u = 0; u < LOADS; ++u) {
-                const int row = ((tid + THREADS * u) % (TILE * 16)) >> 4;
-                if (TILE * t + row >= key_end) stg[u] = u4{0u, 0u, 0u, 0u};
-            }
-        }
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int u = 0; u < LOADS; ++u) {
-            const int q = tid + THREADS * u;
-            *reinterpret_cast<u4*>(&s_kv[buf][16 * q]) = stg[u];
+            const char* src = (half ? pv : pk) + ((row >> 4) ? b1 : b0) + (int64_t)(row & 15) * (KVW * 2) + 16 * chunk;
+            if (tail && TILE * t + row >= key_end) src = reinterpret_cast<const char*>(&g_zero16);
+            dma16(src, &s_kv[buf][16 * (THREADS * u + 64 * wave)]);
         }
     };
 
-    if (n_tiles > 0) load_tile(0);
+    if (n_tiles > 0) load_tile(0, 0);
+    if (NBUF > 2 && n_tiles > 1) load_tile(1, 1);
 
     // ---- Q^T operands: lane (g,c) of block b holds column col0 + 16b + c ----
     h8 qh[NB][4];
@@ -361,12 +393,15 @@ prefill_kernel(PrefillArgs a) {
         for (int cb = 0; cb < 8; ++cb) voff[cb] = swz(vr, 2 * cb + vh) + 8 * (c & 1);
     }
 
-    if (n_tiles > 0) store_tile(0);
-    __syncthreads();
+    if (NBUF > 2 && n_tiles > 1) tile_barrier<LOADS>();
+    else tile_barrier<0>();
 
+    int buf = 0;                                             // t % NBUF
     for (int t = 0; t < n_tiles; ++t) {
-        if (t + 1 < n_tiles) load_tile(t + 1);
-        const unsigned char* sk = s_kv[t & 1];
+        // the tile NBUF-1 ahead goes to the buffer read in iteration t-1
+        const bool ahead = t + NBUF - 1 < n_tiles;
+        if (ahead) load_tile(t + NBUF - 1, buf == 0 ? NBUF - 1 : buf - 1);
+        const unsigned char* sk = s_kv[buf];
         const unsigned char* sv = sk + TILE * ROWB;
         const int key_base = t * TILE;
         // one tile: kMask selects the causal / tail masking (only the tiles
@@ -443,10 +478,9 @@ prefill_kernel(PrefillArgs a) {
             if (key_base + TILE <= key_min_full) tile(std::integral_constant<bool, false>{});
             else tile(std::integral_constant<bool, true>{});
         }
-        if (t + 1 < n_tiles) {
-            store_tile((t + 1) & 1);
-        }
-        __syncthreads();
+        if (NBUF > 2 && ahead) tile_barrier<LOADS * (NBUF - 2)>();
+        else tile_barrier<0>();
+        buf = buf == NBUF - 1 ? 0 : buf + 1;
     }
 
     // ---- normalise and store: lane (g,c) of block b holds d = 16cb + 4g + i ----

@@ -15,8 +15,10 @@
 //    wave per SIMD with 4 blocks).
 //  * K/V tiles of 32 keys (2 pages) are staged ONCE per workgroup in LDS by
 //    direct global->LDS loads (global_load_lds_dwordx4: no staging
-//    registers), NBUF buffers deep: tiles t+1 .. t+NBUF-1 are in flight while
-//    tile t is computed; one barrier per tile.
+//    registers), four buffers: while tile t's softmax runs, the scores of
+//    tile t+1 are on the matrix core and tiles t+2, t+3 are loading; one
+//    barrier per tile.  The loop is unrolled by four so that every LDS
+//    operand address is a lane offset plus a compile-time constant.
 //    Rows keep their 256 B but the 16 B chunks are XOR-swizzled by row
 //    (chunk k of row r at position k ^ (r & 15)), so both operand reads below
 //    are free of LDS bank conflicts.
@@ -30,8 +32,8 @@
 //    at, so lane s of group g points at key row 4g + (s >> 2), halfs
 //    d0 + 4 (s & 3) .. +3, and receives V[4g + j][d0 + s], j = 0..3.
 //  * Rows past the workgroup's last key (unwritten slots may hold NaN bits)
-//    are loaded from a zero row instead, so masked weights never meet NaN
-//    operands.
+//    are loaded from the last key's row instead, so masked weights never
+//    meet NaN operands.
 //  * Q is converted to fp16 once (scaled by 1/sqrt(HD)*log2 e); P is fp16;
 //    accumulation is fp32.  The row sums l come from the matrix core too
 //    (one MFMA of an all-ones operand with P^T per block), so they are the
@@ -72,11 +74,7 @@ typedef __fp16 tr4 __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef __attribute__((address_space(3))) tr4 lds_tr4;
 
 constexpr int NH = Model::NH, NKV = Model::NKV, HD = Model::HD, G = Model::G, KVW = Model::KVW;
-#ifndef NOVA_PREFILL_NBUF
-#define NOVA_PREFILL_NBUF 3
-#endif
-constexpr int NBUF = NOVA_PREFILL_NBUF;        // K/V tile buffers in LDS
-static_assert(NBUF == 2 || NBUF == 3, "two or three tile buffers");
+constexpr int NBUF = 4;                        // K/V tile buffers in LDS
 constexpr int WAVES = 4;
 constexpr int THREADS = WAVES * 64;
 constexpr int NB = 2;                          // 16-column blocks per wave
@@ -88,6 +86,7 @@ constexpr int STAGE_BYTES = 2 * TILE * ROWB;   // K then V
 constexpr int CHUNKS = STAGE_BYTES / 16;       // 16 B chunks per stage
 constexpr int LOADS = CHUNKS / THREADS;        // staging loads per thread per tile
 static_assert(CHUNKS % THREADS == 0, "stage must split evenly over the workgroup");
+static_assert(THREADS == 256 && LOADS == 4, "staging layout: one page row per 16 lanes, K then V");
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazy = 8.0f;                  // rescale threshold, log2 units
 constexpr int64_t kPageBytes = (int64_t)kKvBlock * KVW * 2;
@@ -97,7 +96,7 @@ constexpr int kXcd = 8;                        // XCDs; workgroup w is dispatche
 constexpr int kXcdPerHead = kXcd / NKV;
 constexpr int kBuckets = 4096;                 // cost histogram (tiles; longer items share the top bucket)
 constexpr int kRankMax = 4096;                  // beyond this many items: natural order
-constexpr int kTabWin = 4096;                   // block-table entries held in LDS
+constexpr int kTabWin = 2048;                   // block-table entries held in LDS
 
 struct PrefillArgs {
     const float* q;            // [n_sess][n_q][NH][HD]
@@ -128,13 +127,13 @@ __device__ __forceinline__ int item_bucket(const PrefillArgs& a, int j, int n_cg
 
 // The item of rank r in decreasing cost order (ties in index order).  Every
 // thread of the workgroup calls it (it has barriers) and gets the same answer.
-// s_i: LDS scratch of kBuckets + THREADS + 8 ints.
+// s_i: LDS scratch of kBuckets + THREADS + 16 ints.
 __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int* s_i) {
     const int N = a.n_sess * n_cg;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int* hist = s_i;
     int* part = s_i + kBuckets;
-    int* res = part + THREADS;          // [0] group, [1] ranks above it, [2] item, [4..7] wave counts
+    int* res = part + THREADS;          // [0] group, [1] ranks above it, [2] item, [4..] wave counts
     for (int b = tid; b < kBuckets; b += THREADS) hist[b] = 0;
     __syncthreads();
     for (int j = tid; j < N; j += THREADS) atomicAdd(&hist[item_bucket(a, j, n_cg, n_cols)], 1);
@@ -145,11 +144,12 @@ __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int* 
     for (int u = 0; u < PER; ++u) sum += hist[PER * tid + u];
     part[tid] = sum;
     __syncthreads();
+    constexpr int GPL = THREADS / 64;   // groups per lane
     if (wave == 0) {
-        // lane l covers groups 4l..4l+3; ranks run from the highest group down
+        // lane l covers groups GPL*l .. GPL*l+GPL-1; ranks run from the highest group down
         int ls = 0;
 #pragma unroll
-        for (int u = 0; u < 4; ++u) ls += part[4 * lane + u];
+        for (int u = 0; u < GPL; ++u) ls += part[GPL * lane + u];
         int incl = ls;                                // sum over lanes >= l
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -158,10 +158,10 @@ __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int* 
         }
         int above = incl - ls;
 #pragma unroll
-        for (int u = 3; u >= 0; --u) {
-            const int gsum = part[4 * lane + u];
+        for (int u = GPL - 1; u >= 0; --u) {
+            const int gsum = part[GPL * lane + u];
             if (r >= above && r < above + gsum) {
-                res[0] = 4 * lane + u;
+                res[0] = GPL * lane + u;
                 res[1] = above;
             }
             above += gsum;
@@ -205,20 +205,21 @@ __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int* 
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
-// 16 zero bytes in global memory: the source of the tail rows' loads
-__device__ __attribute__((aligned(16))) u4 g_zero16;
-
-// direct 16 B per lane global -> LDS load; the wave writes 1 KiB at lds (uniform).
+// direct 16 B per lane global -> LDS load; the wave writes 1 KiB at LDS byte
+// address lds (wave-uniform).
 // Issued as inline asm so that the compiler's own vmcnt bookkeeping does not
 // see it: the builtin makes the compiler drain every pending load (including
 // the tiles still meant to be in flight) before each LDS read it cannot prove
 // disjoint.  The pipeline waits for these loads explicitly (tile_barrier);
 // the compiler's waits for its own loads stay correct, as the counter drains
 // in issue order.
-__device__ __forceinline__ void dma16(const void* src, unsigned char* lds) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned char*)lds);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m0) : "memory", "m0");
+__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+}
+
+// LDS byte address of a __shared__ location
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char*)p;
 }
 
 // workgroup barrier for the tile pipeline: the wave's own direct loads of the
@@ -262,11 +263,12 @@ __device__ __forceinline__ uint32_t swz(int row, int chunk) {
 
 // two workgroups per CU (<= 256 registers per wave): while one wave runs its
 // softmax on the VALU the other wave of the SIMD keeps the matrix core busy
-__global__ void __launch_bounds__(THREADS, 2)
+__global__ void __launch_bounds__(THREADS, 2)   // 2 waves per SIMD: <= 256 VGPRs
 prefill_kernel(PrefillArgs a) {
     __shared__ __attribute__((aligned(16))) unsigned char s_kv[NBUF][STAGE_BYTES];
     __shared__ int32_t s_tab[kTabWin];
-    static_assert((kBuckets + THREADS + 8) * 4 <= (int)sizeof(s_kv), "ranking scratch fits the tile buffers");
+    static_assert((kBuckets + THREADS + 16) * 4 <= (int)sizeof(s_kv), "ranking scratch fits the tile buffers");
+    static_assert(4 + WAVES <= 16 && kBuckets % THREADS == 0, "ranking scratch layout");
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -300,14 +302,20 @@ prefill_kernel(PrefillArgs a) {
     const int wave_key_end = col0 < n_cols ? n_past + wave_last / G + 1 : 0;
     const int key_min_full = n_past + col0 / G + 1;           // keys below: visible to all columns
 
-    // ---- staging: which 16 B chunks this thread moves for a tile ----
-    // chunk q = tid + THREADS*u: half = q / (TILE*16) (K or V), row = q%512 / 16,
-    // position p = q % 16 holds global chunk p ^ (row & 15).  All lanes of one
-    // load instruction sit in the same page, so the page base is wave-uniform.
+    // ---- staging ----
+    // Stage chunk q = tid + THREADS*u (u = 0..3): K for u < 2, V for u >= 2;
+    // page u & 1 of the tile; row (tid >> 4) of that page; LDS position
+    // tid & 15 of the row holds global chunk (tid & 15) ^ (tid >> 4).  So a
+    // lane's offset inside a page is the same for all four loads, and each
+    // load instruction of a wave covers 4 rows of one page (wave-uniform base).
     const char* pk = reinterpret_cast<const char*>(a.pool_k);
     const char* pv = reinterpret_cast<const char*>(a.pool_v);
     const int64_t layer_page0 = (int64_t)a.layer * a.nb;
     const int n_pages = (key_end + kKvBlock - 1) >> kKvBlockShift;
+    const int srow = tid >> 4;                               // row inside the page
+    const int schunk = (tid & 15) ^ srow;                    // global chunk this lane moves
+    const uint32_t loff = (uint32_t)(srow * (KVW * 2) + 16 * schunk);
+    const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);
     int win0 = 0;                                            // first page of the LDS table window
     auto load_window = [&](int first) {                      // every thread, uniform
         for (int e = tid; e < kTabWin && first + e < n_pages; e += THREADS) s_tab[e] = table[first + e];
@@ -315,36 +323,49 @@ prefill_kernel(PrefillArgs a) {
         win0 = first;
     };
     load_window(0);
-    // physical page of logical page pg; the window only moves forward, one
-    // tile at a time, and all waves move it together (between two barriers)
-    auto phys_of = [&](int pg) -> int {
-        if (pg - win0 >= kTabWin) {
+    // physical pages of tile T, read from the LDS table a step before the
+    // loads that use them (the window only moves forward, between barriers,
+    // with every wave calling this at the same point)
+    struct Pages { int p0, p1; };
+    auto read_pages = [&](int T) -> Pages {
+        const int pg0 = 2 * T;
+        if (pg0 - win0 >= kTabWin) {
             __syncthreads();                                 // every wave is done with the old window
-            load_window(pg);
+            load_window(pg0);
         }
-        return s_tab[pg - win0];
-    };
-    auto load_tile = [&](int t, int buf) {
-        const int pg0 = 2 * t;
         const int pg1 = pg0 + 1 < n_pages ? pg0 + 1 : pg0;   // a lone last page loads itself twice
-        const int64_t b0 = (layer_page0 + phys_of(pg0)) * kPageBytes + kvh * ROWB;
-        const int64_t b1 = (layer_page0 + phys_of(pg1)) * kPageBytes + kvh * ROWB;
-        const bool tail = TILE * (t + 1) > key_end;         // the tile holding the last key
+        return Pages{s_tab[pg0 - win0], s_tab[pg1 - win0]};
+    };
+    auto load_tile = [&](auto buf_tag, int T, Pages pp) {
+        constexpr int BI = decltype(buf_tag)::value;
+        const int64_t b0 = (layer_page0 + __builtin_amdgcn_readfirstlane(pp.p0)) * kPageBytes + kvh * ROWB;
+        const int64_t b1 = (layer_page0 + __builtin_amdgcn_readfirstlane(pp.p1)) * kPageBytes + kvh * ROWB;
+        const uint32_t m0base = lds_addr(&s_kv[BI][0]) + 1024u * wave_s;
+        if (TILE * (T + 1) <= key_end) {
 #pragma unroll
-        for (int u = 0; u < LOADS; ++u) {
-            const int q = tid + THREADS * u;                 // LDS chunk q of the stage
-            const int half = q / (TILE * 16);
-            const int row = (q % (TILE * 16)) >> 4;
-            const int p = q & 15;
-            const int chunk = p ^ (row & 15);
-            const char* src = (half ? pv : pk) + ((row >> 4) ? b1 : b0) + (int64_t)(row & 15) * (KVW * 2) + 16 * chunk;
-            if (tail && TILE * t + row >= key_end) src = reinterpret_cast<const char*>(&g_zero16);
-            dma16(src, &s_kv[buf][16 * (THREADS * u + 64 * wave)]);
+            for (int u = 0; u < LOADS; ++u)
+                dma16((u < 2 ? pk : pv) + ((u & 1) ? b1 : b0) + loff, m0base + 16u * THREADS * u);
+        } else {
+            // the tile holding the last key: rows past it (never written, may
+            // hold NaN bits) load the last key's row instead; their weights are
+            // masked to zero
+            const int rl = key_end - 1 - TILE * T;           // in [0, TILE)
+            const int64_t bl = ((rl >> 4) ? b1 : b0) + (int64_t)((rl & 15) * (KVW * 2) + 16 * schunk);
+#pragma unroll
+            for (int u = 0; u < LOADS; ++u) {
+                const int row = srow + 16 * (u & 1);
+                const char* pool = u < 2 ? pk : pv;
+                dma16(TILE * T + row < key_end ? pool + ((u & 1) ? b1 : b0) + loff : pool + bl,
+                      m0base + 16u * THREADS * u);
+            }
         }
     };
 
-    if (n_tiles > 0) load_tile(0, 0);
-    if (NBUF > 2 && n_tiles > 1) load_tile(1, 1);
+    Pages pp{0, 0};
+    if (n_tiles > 0) load_tile(std::integral_constant<int, 0>{}, 0, read_pages(0));
+    if (n_tiles > 1) load_tile(std::integral_constant<int, 1>{}, 1, read_pages(1));
+    if (n_tiles > 2) load_tile(std::integral_constant<int, 2>{}, 2, read_pages(2));
+    if (n_tiles > 3) pp = read_pages(3);
 
     // ---- Q^T operands: lane (g,c) of block b holds column col0 + 16b + c ----
     h8 qh[NB][4];
@@ -383,104 +404,131 @@ prefill_kernel(PrefillArgs a) {
         for (int cb = 0; cb < 8; ++cb) acc[b][cb] = f4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // V^T operand addresses: lane s of group g reads key row 4g + (s >> 2) (and
-    // +16, the second page), halfs 16cb + 4 (s & 3) .. +3 of it
-    uint32_t voff[8];
+    // operand addresses inside a stage (the buffer adds a compile-time offset):
+    // K rows c (page 0) and 16 + c (page 1), chunk 4ks + g; V^T: lane s of
+    // group g reads key row 4g + (s >> 2) (and +16, the second page), halfs
+    // 16cb + 4 (s & 3) .. +3 of it
+    uint32_t koff[4], voff[8];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) koff[ks] = swz(c, 4 * ks + g);
     {
         const int vr = 4 * g + (c >> 2);
         const int vh = (c >> 1) & 1;
 #pragma unroll
-        for (int cb = 0; cb < 8; ++cb) voff[cb] = swz(vr, 2 * cb + vh) + 8 * (c & 1);
+        for (int cb = 0; cb < 8; ++cb) voff[cb] = TILE * ROWB + swz(vr, 2 * cb + vh) + 8 * (c & 1);
     }
 
-    if (NBUF > 2 && n_tiles > 1) tile_barrier<LOADS>();
+    // tiles 0 and 1 resident (tile 2 may still be loading)
+    if (n_tiles > 2) tile_barrier<LOADS>();
     else tile_barrier<0>();
 
-    int buf = 0;                                             // t % NBUF
-    for (int t = 0; t < n_tiles; ++t) {
-        // the tile NBUF-1 ahead goes to the buffer read in iteration t-1
-        const bool ahead = t + NBUF - 1 < n_tiles;
-        if (ahead) load_tile(t + NBUF - 1, buf == 0 ? NBUF - 1 : buf - 1);
-        const unsigned char* sk = s_kv[buf];
-        const unsigned char* sv = sk + TILE * ROWB;
-        const int key_base = t * TILE;
-        // one tile: kMask selects the causal / tail masking (only the tiles
-        // that cross the diagonal or the end of the keys need it)
-        auto tile = [&](auto mask_tag) {
-            constexpr bool kMask = decltype(mask_tag)::value;
-
-            // S^T = K . Q^T for both pages and all blocks
-            f4 s0[NB], s1[NB];
+    // S^T = K . Q^T for both pages of the tile in buffer BI and all blocks
+    auto compute_s = [&](auto buf_tag, f4 (&s0)[NB], f4 (&s1)[NB]) {
+        constexpr int BI = decltype(buf_tag)::value;
+        const unsigned char* sk = s_kv[BI];
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                s0[b] = f4{0.f, 0.f, 0.f, 0.f};
-                s1[b] = f4{0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const h8 k0 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + swz(c, 4 * ks + g)));
-                const h8 k1 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + swz(16 + c, 4 * ks + g)));
-#pragma unroll
-                for (int b = 0; b < NB; ++b) {
-                    s0[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qh[b][ks], s0[b], 0, 0, 0);
-                    s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[b][ks], s1[b], 0, 0, 0);
-                }
-            }
-            // V^T operands: va[cb] row c = d 16cb + c, k = keys kappa(g, j) =
-            // (page j / 4, slot 4g + j % 4), the k order of P^T below
-            h8 va[8];
-#pragma unroll
-            for (int cb = 0; cb < 8; ++cb) {
-                const u2 lo = lds_read_tr(sv + voff[cb]);
-                const u2 hi = lds_read_tr(sv + voff[cb] + 16 * ROWB);
-                va[cb] = __builtin_bit_cast(h8, u4{lo[0], lo[1], hi[0], hi[1]});
-            }
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                float sc[8];
-                bool ok[8];
-#pragma unroll
-                for (int ii = 0; ii < 4; ++ii) {
-                    sc[ii] = s0[b][ii];
-                    sc[4 + ii] = s1[b][ii];
-                }
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int key = key_base + (j < 4 ? 0 : 16) + 4 * g + (j & 3);
-                    ok[j] = !kMask || key <= qpos[b];
-                }
-                float bm = -INFINITY;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) bm = ok[j] ? fmaxf(bm, sc[j]) : bm;
-                bm = rows_max(bm);
-                const bool need = bm > m[b] + kLazy;
-                if (__builtin_amdgcn_ballot_w64(need)) {
-                    const float mn = need ? bm : m[b];
-                    const float corr = __builtin_amdgcn_exp2f(m[b] - mn);
-                    lsum[b] *= corr;
-#pragma unroll
-                    for (int cb = 0; cb < 8; ++cb) acc[b][cb] *= corr;
-                    m[b] = mn;
-                }
-                h8 ph;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) ph[j] = (_Float16)(ok[j] ? __builtin_amdgcn_exp2f(sc[j] - m[b]) : 0.f);
-                // l += ones . P^T: the sum of exactly the fp16 weights applied below
-                lsum[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph, lsum[b], 0, 0, 0);
-#pragma unroll
-                for (int cb = 0; cb < 8; ++cb)
-                    acc[b][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[cb], ph, acc[b][cb], 0, 0, 0);
-            }
-        };
-        if (key_base < wave_key_end) {
-            // a tile needs no mask when every key in it exists and is visible to
-            // every column of the wave
-            if (key_base + TILE <= key_min_full) tile(std::integral_constant<bool, false>{});
-            else tile(std::integral_constant<bool, true>{});
+        for (int b = 0; b < NB; ++b) {
+            s0[b] = f4{0.f, 0.f, 0.f, 0.f};
+            s1[b] = f4{0.f, 0.f, 0.f, 0.f};
         }
-        if (NBUF > 2 && ahead) tile_barrier<LOADS * (NBUF - 2)>();
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const h8 k0 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + koff[ks]));
+            const h8 k1 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + koff[ks] + 16 * ROWB));
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                s0[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qh[b][ks], s0[b], 0, 0, 0);
+                s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[b][ks], s1[b], 0, 0, 0);
+            }
+        }
+    };
+    // online softmax of one tile's scores and O^T += V^T . P^T; kMask selects
+    // the causal masking (only the tiles that cross the diagonal or the end of
+    // the keys need it)
+    auto softmax_pv = [&](auto mask_tag, auto buf_tag, int key_base, const f4 (&s0)[NB], const f4 (&s1)[NB]) {
+        constexpr bool kMask = decltype(mask_tag)::value;
+        constexpr int BI = decltype(buf_tag)::value;
+        const unsigned char* sv = s_kv[BI];
+        // V^T operands: va[cb] row c = d 16cb + c, k = keys kappa(g, j) =
+        // (page j / 4, slot 4g + j % 4), the k order of P^T below
+        h8 va[8];
+#pragma unroll
+        for (int cb = 0; cb < 8; ++cb) {
+            const u2 lo = lds_read_tr(sv + voff[cb]);
+            const u2 hi = lds_read_tr(sv + voff[cb] + 16 * ROWB);
+            va[cb] = __builtin_bit_cast(h8, u4{lo[0], lo[1], hi[0], hi[1]});
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            float sc[8];
+            bool ok[8];
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+                sc[ii] = s0[b][ii];
+                sc[4 + ii] = s1[b][ii];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int key = key_base + (j < 4 ? 0 : 16) + 4 * g + (j & 3);
+                ok[j] = !kMask || key <= qpos[b];
+            }
+            float bm = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) bm = ok[j] ? fmaxf(bm, sc[j]) : bm;
+            bm = rows_max(bm);
+            const bool need = bm > m[b] + kLazy;
+            if (__builtin_amdgcn_ballot_w64(need)) {
+                const float mn = need ? bm : m[b];
+                const float corr = __builtin_amdgcn_exp2f(m[b] - mn);
+                lsum[b] *= corr;
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb) acc[b][cb] *= corr;
+                m[b] = mn;
+            }
+            h8 ph;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ph[j] = (_Float16)(ok[j] ? __builtin_amdgcn_exp2f(sc[j] - m[b]) : 0.f);
+            // l += ones . P^T: the sum of exactly the fp16 weights applied below
+            lsum[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph, lsum[b], 0, 0, 0);
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb)
+                acc[b][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[cb], ph, acc[b][cb], 0, 0, 0);
+        }
+    };
+
+    // Tile pipeline over NBUF = 4 buffers.  Step t (buffer t % 4): issue the
+    // loads of tile t+3 into the buffer of tile t-1 and read tile t+4's pages;
+    // issue the score MFMAs of tile t+1; run tile t's softmax and PV, so the
+    // softmax VALU work overlaps the matrix core's work on tile t+1; then the
+    // barrier makes tile t+2 resident (tile t+3 may stay in flight).
+    const int wave_tiles = (wave_key_end + TILE - 1) / TILE;   // tiles this wave computes
+    f4 sa0[NB], sa1[NB], sb0[NB], sb1[NB];
+    if (wave_tiles > 0) compute_s(std::integral_constant<int, 0>{}, sa0, sa1);
+    auto step = [&](auto buf_tag, int t, f4 (&c0)[NB], f4 (&c1)[NB], f4 (&n0)[NB], f4 (&n1)[NB]) {
+        constexpr int BI = decltype(buf_tag)::value;
+        const bool ahead = t + 3 < n_tiles;
+        if (ahead) {
+            load_tile(std::integral_constant<int, (BI + 3) % NBUF>{}, t + 3, pp);
+            if (t + 4 < n_tiles) pp = read_pages(t + 4);
+        }
+        if (t < wave_tiles) {
+            if (t + 1 < wave_tiles) compute_s(std::integral_constant<int, (BI + 1) % NBUF>{}, n0, n1);
+            const int key_base = t * TILE;
+            // a tile needs no mask when every key in it exists and is visible
+            // to every column of the wave
+            if (key_base + TILE <= key_min_full)
+                softmax_pv(std::integral_constant<bool, false>{}, buf_tag, key_base, c0, c1);
+            else
+                softmax_pv(std::integral_constant<bool, true>{}, buf_tag, key_base, c0, c1);
+        }
+        if (ahead) tile_barrier<LOADS>();
         else tile_barrier<0>();
-        buf = buf == NBUF - 1 ? 0 : buf + 1;
+    };
+    for (int t = 0; t < n_tiles; t += NBUF) {               // unrolled: buffers and score registers rotate
+        step(std::integral_constant<int, 0>{}, t, sa0, sa1, sb0, sb1);
+        if (t + 1 < n_tiles) step(std::integral_constant<int, 1>{}, t + 1, sb0, sb1, sa0, sa1);
+        if (t + 2 < n_tiles) step(std::integral_constant<int, 2>{}, t + 2, sa0, sa1, sb0, sb1);
+        if (t + 3 < n_tiles) step(std::integral_constant<int, 3>{}, t + 3, sb0, sb1, sa0, sa1);
     }
 
     // ---- normalise and store: lane (g,c) of block b holds d = 16cb + 4g + i ----

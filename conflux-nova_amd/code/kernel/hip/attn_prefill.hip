@@ -38,12 +38,14 @@
 //    accumulation is fp32.  The row sums l come from the matrix core too
 //    (one MFMA of an all-ones operand with P^T per block), so they are the
 //    sums of exactly the fp16 weights applied to V, at no VALU cost.
-//  * Lazy rescaling: a column's running max only moves when a tile's max
+//  * Lazy rescaling: a column's running max m only moves when a tile's max
 //    exceeds it by more than 8 (log2 units), bounding P by 2^8 in fp16, so the
-//    O rescale (32 multiplies per block) is skipped on most tiles.
-//  * Softmax statistics cross the four 16-lane rows with v_permlane16/32_swap
-//    (no LDS round trip) and use the raw v_exp_f32; tiles wholly below the
-//    causal diagonal run a mask-free path.
+//    O rescale (32 multiplies per block) is skipped on most tiles.  The score
+//    MFMAs start from -m (accumulator seed), so they yield s - m directly; the
+//    common case is one lane-local comparison against 8 and a wave ballot,
+//    and only a rescale takes the row max across the four 16-lane rows
+//    (v_permlane16/32_swap, no LDS round trip).  Exponentials use the raw
+//    v_exp_f32; tiles wholly below the causal diagonal run a mask-free path.
 //  * The workgroup's slice of the block table sits in LDS (windows of 4096
 //    pages), so a page lookup never waits on the vector-memory counter that
 //    the tile loads in flight occupy; causal masking is per (key, column);
@@ -390,7 +392,11 @@ prefill_kernel(PrefillArgs a) {
         }
     }
 
+    // Running max m of the lane's column (log2 units), kept as -m in the four
+    // lanes' accumulator seeds: the score MFMAs start from -m, so they produce
+    // s - m directly.  m starts at 0; the wave's first tile always rescales.
     float m[NB];
+    f4 negm[NB];
     f4 lsum[NB];          // row sums from the matrix core: every element = l of column c
     f4 acc[NB][8];
     h8 ones;
@@ -398,7 +404,8 @@ prefill_kernel(PrefillArgs a) {
     for (int j = 0; j < 8; ++j) ones[j] = (_Float16)1.0f;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        m[b] = -INFINITY;
+        m[b] = 0.f;
+        negm[b] = f4{0.f, 0.f, 0.f, 0.f};
         lsum[b] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) acc[b][cb] = f4{0.f, 0.f, 0.f, 0.f};
@@ -427,25 +434,23 @@ prefill_kernel(PrefillArgs a) {
         constexpr int BI = decltype(buf_tag)::value;
         const unsigned char* sk = s_kv[BI];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            s0[b] = f4{0.f, 0.f, 0.f, 0.f};
-            s1[b] = f4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const h8 k0 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + koff[ks]));
             const h8 k1 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + koff[ks] + 16 * ROWB));
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                s0[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qh[b][ks], s0[b], 0, 0, 0);
-                s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[b][ks], s1[b], 0, 0, 0);
+                s0[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qh[b][ks], ks ? s0[b] : negm[b], 0, 0, 0);
+                s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[b][ks], ks ? s1[b] : negm[b], 0, 0, 0);
             }
         }
     };
-    // online softmax of one tile's scores and O^T += V^T . P^T; kMask selects
-    // the causal masking (only the tiles that cross the diagonal or the end of
-    // the keys need it)
-    auto softmax_pv = [&](auto mask_tag, auto buf_tag, int key_base, const f4 (&s0)[NB], const f4 (&s1)[NB]) {
+    // One tile: online softmax of the scores c (buffer BI) and O^T += V^T . P^T,
+    // with the next tile's score MFMAs (buffer NI, into n) issued in the same
+    // basic block as this tile's row maxima so that the matrix core and the
+    // VALU work side by side.  kMask selects the causal masking (only tiles
+    // that cross the diagonal or the end of the keys need it).
+    auto tile = [&](auto mask_tag, auto buf_tag, auto next_tag, int key_base, const f4 (&c0)[NB],
+                    const f4 (&c1)[NB], f4 (&n0)[NB], f4 (&n1)[NB]) {
         constexpr bool kMask = decltype(mask_tag)::value;
         constexpr int BI = decltype(buf_tag)::value;
         const unsigned char* sv = s_kv[BI];
@@ -458,49 +463,76 @@ prefill_kernel(PrefillArgs a) {
             const u2 hi = lds_read_tr(sv + voff[cb] + 16 * ROWB);
             va[cb] = __builtin_bit_cast(h8, u4{lo[0], lo[1], hi[0], hi[1]});
         }
+        compute_s(next_tag, n0, n1);
+        // x = s - m; the common case only asks whether any score of the wave
+        // exceeds its column's max by more than kLazy (a lane-local test)
+        float x[NB][8];
+        bool ok[NB][8];
+        float lmax[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            float sc[8];
-            bool ok[8];
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-                sc[ii] = s0[b][ii];
-                sc[4 + ii] = s1[b][ii];
+                x[b][ii] = c0[b][ii];
+                x[b][4 + ii] = c1[b][ii];
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int key = key_base + (j < 4 ? 0 : 16) + 4 * g + (j & 3);
-                ok[j] = !kMask || key <= qpos[b];
+                ok[b][j] = !kMask || key <= qpos[b];
             }
-            float bm = -INFINITY;
+            float v = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) bm = ok[j] ? fmaxf(bm, sc[j]) : bm;
-            bm = rows_max(bm);
-            const bool need = bm > m[b] + kLazy;
-            if (__builtin_amdgcn_ballot_w64(need)) {
-                const float mn = need ? bm : m[b];
-                const float corr = __builtin_amdgcn_exp2f(m[b] - mn);
+            for (int j = 0; j < 8; ++j) v = ok[b][j] ? fmaxf(v, x[b][j]) : v;
+            lmax[b] = v;
+        }
+        // score MFMAs of the next tile interleaved with the tests above
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);   // one VALU
+        }
+        if (__builtin_amdgcn_ballot_w64(lmax[0] > kLazy || lmax[1] > kLazy) || key_base == 0) {
+            // rare (and the first tile): move the max of every column whose
+            // tile max exceeds it by more than kLazy.  bm = -inf: no key of the
+            // column in this tile, nothing moves.
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const float bm = rows_max(lmax[b]);
+                const bool need = bm > -INFINITY && (key_base == 0 || bm > kLazy);
+                const float shift = need ? bm : 0.f;
+                const float corr = key_base == 0 ? 0.f : __builtin_amdgcn_exp2f(-shift);
                 lsum[b] *= corr;
 #pragma unroll
                 for (int cb = 0; cb < 8; ++cb) acc[b][cb] *= corr;
-                m[b] = mn;
-            }
-            h8 ph;
+                m[b] += shift;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) ph[j] = (_Float16)(ok[j] ? __builtin_amdgcn_exp2f(sc[j] - m[b]) : 0.f);
+                for (int j = 0; j < 8; ++j) x[b][j] -= shift;
+                n0[b] -= shift;                  // the next tile's scores were seeded with the old max
+                n1[b] -= shift;
+                negm[b] = f4{-m[b], -m[b], -m[b], -m[b]};
+            }
+        }
+        h8 ph[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                ph[b][j] = (_Float16)(ok[b][j] ? __builtin_amdgcn_exp2f(x[b][j]) : 0.f);
             // l += ones . P^T: the sum of exactly the fp16 weights applied below
-            lsum[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph, lsum[b], 0, 0, 0);
+            lsum[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph[b], lsum[b], 0, 0, 0);
 #pragma unroll
             for (int cb = 0; cb < 8; ++cb)
-                acc[b][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[cb], ph, acc[b][cb], 0, 0, 0);
+                acc[b][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[cb], ph[b], acc[b][cb], 0, 0, 0);
         }
     };
 
     // Tile pipeline over NBUF = 4 buffers.  Step t (buffer t % 4): issue the
     // loads of tile t+3 into the buffer of tile t-1 and read tile t+4's pages;
-    // issue the score MFMAs of tile t+1; run tile t's softmax and PV, so the
-    // softmax VALU work overlaps the matrix core's work on tile t+1; then the
-    // barrier makes tile t+2 resident (tile t+3 may stay in flight).
+    // run tile t (its softmax and PV, with tile t+1's score MFMAs alongside);
+    // then the barrier makes tile t+2 resident (tile t+3 may stay in flight).
+    // A wave's last tile computes scores of a buffer it will not use: they are
+    // discarded.
     const int wave_tiles = (wave_key_end + TILE - 1) / TILE;   // tiles this wave computes
     f4 sa0[NB], sa1[NB], sb0[NB], sb1[NB];
     if (wave_tiles > 0) compute_s(std::integral_constant<int, 0>{}, sa0, sa1);
@@ -512,14 +544,14 @@ prefill_kernel(PrefillArgs a) {
             if (t + 4 < n_tiles) pp = read_pages(t + 4);
         }
         if (t < wave_tiles) {
-            if (t + 1 < wave_tiles) compute_s(std::integral_constant<int, (BI + 1) % NBUF>{}, n0, n1);
             const int key_base = t * TILE;
+            constexpr auto next = std::integral_constant<int, (BI + 1) % NBUF>{};
             // a tile needs no mask when every key in it exists and is visible
             // to every column of the wave
             if (key_base + TILE <= key_min_full)
-                softmax_pv(std::integral_constant<bool, false>{}, buf_tag, key_base, c0, c1);
+                tile(std::integral_constant<bool, false>{}, buf_tag, next, key_base, c0, c1, n0, n1);
             else
-                softmax_pv(std::integral_constant<bool, true>{}, buf_tag, key_base, c0, c1);
+                tile(std::integral_constant<bool, true>{}, buf_tag, next, key_base, c0, c1, n0, n1);
         }
         if (ahead) tile_barrier<LOADS>();
         else tile_barrier<0>();

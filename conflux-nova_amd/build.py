@@ -35,6 +35,7 @@ HIP_SOURCES = [
     "code/kernel/hip/attn_decode.hip",
     "code/kernel/hip/attn_prefill.hip",
     "code/kernel/hip/kv_pages.hip",
+    "code/kernel/hip/rope.hip",
     "code/kernel/hip/testkit.hip",
 ]
 CXX_SOURCES = [

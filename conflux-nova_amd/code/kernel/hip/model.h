@@ -13,22 +13,23 @@
 
 namespace nova {
 
-template <int NH_, int NKV_, int HD_, int L_>
+template <int NH_, int NKV_, int HD_, int L_, int THETA_>
 struct Geometry {
     static constexpr int NH = NH_, NKV = NKV_, HD = HD_, L = L_;
+    static constexpr int kTheta = THETA_;       // RoPE base (matrix.h:46-50: 1e6 for Qwen2.5)
     static constexpr int G = NH / NKV;          // GQA group
     static constexpr int KVW = NKV * HD;        // halves per token per pool
     static_assert(NH % NKV == 0, "GQA heads must divide");
 };
 
 #if defined(NOVA_MODEL_QWEN25_7B)
-using Model = Geometry<28, 4, 128, 28>;
+using Model = Geometry<28, 4, 128, 28, 1000000>;
 inline constexpr const char* kModelName = "Qwen2.5-7B";
 #elif defined(NOVA_MODEL_QWEN25_1P5B)
-using Model = Geometry<12, 2, 128, 28>;
+using Model = Geometry<12, 2, 128, 28, 1000000>;
 inline constexpr const char* kModelName = "Qwen2.5-1.5B";
 #elif defined(NOVA_MODEL_QWEN25_14B)
-using Model = Geometry<40, 8, 128, 48>;
+using Model = Geometry<40, 8, 128, 48, 1000000>;
 inline constexpr const char* kModelName = "Qwen2.5-14B";
 #else
 #error "no model selected: pass -DNOVA_MODEL_QWEN25_7B, _1P5B or _14B"

@@ -137,6 +137,37 @@ void launch_kv_zero_pages(uint16_t* pool_k, uint16_t* pool_v, int nb, const int3
 void launch_table_patch(int32_t* table_dev, const int32_t* idx, const int32_t* val, int n,
                         nova_stream_t s);
 
+/* ---- RoPE (src/kernel/rope.cu), NeoX pairs (i, i+HD/2) of the Qwen2 family ---- */
+
+/* cos/sin table [4096][HD/2] fp32 (the reference's kCtx rows, config.h:23).
+ * Replaces nova::launch_rope_table, include/nova/kernel.h:47 (rope.cu:9-18,69-72).
+ * Each float step of the reference recipe is correctly rounded. */
+void launch_rope_table(float* cs, float* sn, nova_stream_t s);
+/* The same table with `rows` positions, for contexts past the reference's
+ * 4096-row table.  Not a reference surface. */
+void launch_rope_table_rows(float* cs, float* sn, int rows, nova_stream_t s);
+/* Rotate n tokens in place: q [n][NH][HD], k [n][NKV][HD] fp32 at positions
+ * pos0..pos0+n-1.  Replaces nova::launch_rope_batch, kernel.h:48 (rope.cu:39-58,74-80). */
+void launch_rope_batch(float* q, float* k, int n, int64_t pos0, const float* cs, const float* sn,
+                       nova_stream_t s);
+/* One token.  Replaces nova::launch_rope, kernel.h:49 (rope.cu:21-37,82-87). */
+void launch_rope(float* q, float* k, int64_t pos, const float* cs, const float* sn, nova_stream_t s);
+/* RopeKvOp fused (code/graph/dense.h:75-83: rope_batch, then kv_store_paged):
+ * rotate q in place; rotate k and append it with v as fp16 at pos0..pos0+n-1
+ * through the block table (k, v: [n][NKV][HD] fp32; k's buffer is left as
+ * passed).  One launch and no round trip of K through memory. */
+void launch_rope_kv_store_paged(float* q, const float* k, const float* v, const float* cs, const float* sn,
+                                uint16_t* pool_k, uint16_t* pool_v, const int32_t* table, int layer, int nb,
+                                int n, int64_t pos0, nova_stream_t s);
+/* Batched form: session i rotates and appends n tokens at n_past[i]..
+ * (device int32[n_sess]) through tables + i*table_stride; q [n_sess][n][NH][HD],
+ * k, v [n_sess][n][NKV][HD] fp32.  A decode step's RoPE + append for all
+ * sessions (n = 1) or a prefill chunk per session, in one launch. */
+void launch_rope_kv_store_paged_batch(float* q, const float* k, const float* v, const float* cs,
+                                      const float* sn, uint16_t* pool_k, uint16_t* pool_v,
+                                      const int32_t* tables, int table_stride, const int32_t* n_past,
+                                      int n_sess, int n, int layer, int nb, nova_stream_t s);
+
 #ifdef __cplusplus
 }
 #endif

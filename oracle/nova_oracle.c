@@ -410,6 +410,66 @@ void or_kv_store_paged(or_geom g, uint16_t* pool_k, uint16_t* pool_v, const int3
     }
 }
 
+/* ---- RoPE ---- */
+void or_rope_table(float* cs, float* sn, int rows, int half, double theta) {
+    /* rope_table_kernel rope.cu:9-18, each float step correctly rounded */
+    const float l2 = (float)log2((double)(float)theta);
+    for (int pos = 0; pos < rows; ++pos) {
+        for (int i = 0; i < half; ++i) {
+            const float e = -(float)i * (1.f / (float)half);
+            const float t = e * l2;
+            const float f = (float)exp2((double)t);
+            const float a = (float)pos * f;
+            cs[(int64_t)pos * half + i] = (float)cos((double)a);
+            sn[(int64_t)pos * half + i] = (float)sin((double)a);
+        }
+    }
+}
+
+static void rope_row(float* base, int half, const float* c, const float* s) {
+    /* rope_batch_kernel rope.cu:51-57 (NeoX: a = i, b = i + half) */
+    for (int i = 0; i < half; ++i) {
+        const float x0 = base[i], x1 = base[i + half];
+        base[i] = x0 * c[i] - x1 * s[i];
+        base[i + half] = x0 * s[i] + x1 * c[i];
+    }
+}
+
+void or_rope_apply(or_geom g, float* q, float* k, int n, int64_t pos0, const float* cs, const float* sn) {
+    /* launch_rope_batch rope.cu:74-80: grid (token, head), heads 0..nh-1 are q, then k */
+    const int half = g.hd / 2;
+    for (int t = 0; t < n; ++t) {
+        const int64_t pos = pos0 + t;
+        const float* c = cs + pos * half;
+        const float* s = sn + pos * half;
+        for (int h = 0; h < g.nh; ++h) rope_row(q + ((int64_t)t * g.nh + h) * g.hd, half, c, s);
+        for (int h = 0; h < g.nkv; ++h) rope_row(k + ((int64_t)t * g.nkv + h) * g.hd, half, c, s);
+    }
+}
+
+void or_rope_kv_store_paged(or_geom g, float* q, const float* k, const float* v, const float* cs,
+                            const float* sn, uint16_t* pool_k, uint16_t* pool_v, const int32_t* table,
+                            int layer, int nb, int n, int64_t pos0) {
+    /* RopeKvOp dense.h:75-83 = launch_rope_batch + launch_kv_store_paged (elem.cu:59-76) */
+    const int half = g.hd / 2;
+    const int64_t kvw = (int64_t)g.nkv * g.hd;
+    float* kr = (float*)malloc(sizeof(float) * (size_t)kvw);
+    for (int t = 0; t < n; ++t) {
+        const int64_t pos = pos0 + t;
+        const float* c = cs + pos * half;
+        const float* s = sn + pos * half;
+        for (int h = 0; h < g.nh; ++h) rope_row(q + ((int64_t)t * g.nh + h) * g.hd, half, c, s);
+        memcpy(kr, k + (int64_t)t * kvw, sizeof(float) * (size_t)kvw);
+        for (int h = 0; h < g.nkv; ++h) rope_row(kr + (int64_t)h * g.hd, half, c, s);
+        const int64_t off = page_base(g, layer, nb, table[pos / g.kb]) + (pos % g.kb) * kvw;
+        for (int64_t e = 0; e < kvw; ++e) {
+            pool_k[off + e] = or_f32_to_f16(kr[e]);
+            pool_v[off + e] = or_f32_to_f16(v[(int64_t)t * kvw + e]);
+        }
+    }
+    free(kr);
+}
+
 void or_kv_gather_paged(or_geom g, const uint16_t* pool, const int32_t* table, int layer, int nb,
                         int64_t n, uint16_t* out) {
     const int64_t kvw = (int64_t)g.nkv * g.hd;

@@ -88,6 +88,25 @@ void or_kv_store_paged(or_geom g, uint16_t* pool_k, uint16_t* pool_v, const int3
 void or_kv_gather_paged(or_geom g, const uint16_t* pool, const int32_t* table, int layer, int nb,
                         int64_t n, uint16_t* out);
 
+/* ---------------- RoPE (src/kernel/rope.cu) ----------------
+ * Table: rope_table_kernel rope.cu:9-18, cs/sn [rows][half] with
+ *   f_i = exp2f(-(float)i * (1/half) * log2f(theta)), a = (float)pos * f_i,
+ *   cs = cosf(a), sn = sinf(a)
+ * evaluated with every float operation correctly rounded (transcendentals in
+ * double, rounded once), which fixes the table bit for bit.
+ * Rotation: rope_batch_kernel rope.cu:39-58, NeoX pairs (i, i + half) for the
+ * Qwen2 family (include/nova/arch/traits.h:15-17), x0*c - x1*s and x0*s + x1*c
+ * without contraction.  q [n][nh][hd] and k [n][nkv][hd] fp32, rotated in place
+ * at positions pos0 .. pos0+n-1. */
+void or_rope_table(float* cs, float* sn, int rows, int half, double theta);
+void or_rope_apply(or_geom g, float* q, float* k, int n, int64_t pos0, const float* cs, const float* sn);
+/* RopeKvOp (code/graph/dense.h:75-83): rope_batch then kv_store_paged, with
+ * the pool in fp16: q rotated in place, k rotated (its buffer untouched) and
+ * appended with v as fp16 (round to nearest even) at pos0 .. pos0+n-1. */
+void or_rope_kv_store_paged(or_geom g, float* q, const float* k, const float* v, const float* cs,
+                            const float* sn, uint16_t* pool_k, uint16_t* pool_v, const int32_t* table,
+                            int layer, int nb, int n, int64_t pos0);
+
 /* ---------------- COW page copy (src/model.cpp:171-191) ---------------- */
 void or_cow_copy(or_geom g, uint16_t* pool_k, uint16_t* pool_v, int n_layers, int nb,
                  int src, int dst);

@@ -121,6 +121,9 @@ class Oracle:
         L.or_attn_prefill_paged.argtypes = [Geom, vp, vp, vp, vp, i32, i32, i32, i32, vp]
         L.or_attn_prefill_paged_f64.argtypes = [Geom, vp, vp, vp, vp, i32, i32, i32, i32, vp]
         L.or_attn_decode_batch.argtypes = [Geom, vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, i32]
+        L.or_rope_table.argtypes = [vp, vp, i32, i32, C.c_double]
+        L.or_rope_apply.argtypes = [Geom, vp, vp, i32, i64, vp, vp]
+        L.or_rope_kv_store_paged.argtypes = [Geom, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i64]
 
     # ---- hashing ----
     def kv_hash_ids(self, ids) -> int:
@@ -168,6 +171,30 @@ class Oracle:
         fn(g, self._p(q), self._p(pool_k), self._p(pool_v), self._p(table), layer, nb, n_q, n_past,
            self._p(out))
         return out
+
+    # ---- RoPE ----
+    def rope_table(self, rows, half=64, theta=1e6):
+        cs = np.empty((rows, half), np.float32)
+        sn = np.empty((rows, half), np.float32)
+        self.lib.or_rope_table(self._p(cs), self._p(sn), rows, half, theta)
+        return cs, sn
+
+    def rope_apply(self, model, q, k, pos0, cs, sn):
+        """Rotate q [n][nh][hd] and k [n][nkv][hd] (fp32, in place copies returned)."""
+        q = np.array(q, np.float32, order="C")
+        k = np.array(k, np.float32, order="C")
+        self.lib.or_rope_apply(geom(model), self._p(q), self._p(k), q.shape[0], pos0, self._p(cs), self._p(sn))
+        return q, k
+
+    def rope_kv_store_paged(self, model, q, k, v, cs, sn, pool_k, pool_v, table, layer, nb, pos0):
+        """Returns the rotated q; pool_k / pool_v are updated in place."""
+        q = np.array(q, np.float32, order="C")
+        k = np.ascontiguousarray(k, np.float32)
+        v = np.ascontiguousarray(v, np.float32)
+        self.lib.or_rope_kv_store_paged(geom(model), self._p(q), self._p(k), self._p(v), self._p(cs), self._p(sn),
+                                        self._p(pool_k), self._p(pool_v), self._p(table), layer, nb,
+                                        q.shape[0], pos0)
+        return q
 
     def attn_decode_batch(self, model, q, pool_k, pool_v, tables, n_keys, layer, nb, n_threads):
         g = geom(model)

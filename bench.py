@@ -17,7 +17,8 @@ kernel measured with HIP events; cpu_baseline = the C oracle on the host cores
 over one layer of the same workload).
 
 Other workloads (--workload): single1p5b (config 1), cow (config 3),
-longctx14b (config 4), prefill (config 5).  They print their own JSON line.
+longctx14b (config 4), prefill (config 5), rope (RoPE fused with the append,
+config-5 chunk shape).  They print their own JSON line.
 """
 from __future__ import annotations
 
@@ -47,7 +48,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="decode7b",
-                    choices=["decode7b", "single1p5b", "cow", "longctx14b", "prefill", "copycal"])
+                    choices=["decode7b", "single1p5b", "cow", "longctx14b", "prefill", "rope", "copycal"])
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
@@ -538,6 +539,108 @@ def run_prefill(args):
     }
 
 
+def rope_bytes(n_tok, nh, nkv, hd) -> int:
+    """Algorithmic bytes of RoPE + fp16 append per token: q read and written
+    (fp32), k and v read (fp32), the cos/sin row read, k and v written (fp16)."""
+    return n_tok * (2 * nh * hd * 4 + 2 * nkv * hd * 4 + 2 * (hd // 2) * 4 + 2 * nkv * hd * 2)
+
+
+def run_rope(args):
+    """RoPE fused with the paged append (launch_rope_kv_store_paged_batch),
+    the step before the attention path (RopeKvOp, code/graph/dense.h:75-83):
+    a config-5-shaped prefill chunk (8 sessions x 512 tokens at n_past
+    U[0,4096]) is the measured launch; a decode step (16 sessions x 1 token)
+    is timed beside it."""
+    nova = nova_amd.load("qwen25_7b")
+    s = nova.dev_stream_create()
+    rng = np.random.default_rng(args.seed)
+    nh, nkv, hd = nova.nh, nova.nkv, nova.hd
+    rows = 16384
+    cs, sn = nova.alloc(rows * hd // 2 * 4), nova.alloc(rows * hd // 2 * 4)
+    nova.launch_rope_table_rows(cs.ptr, sn.ptr, rows, s)
+
+    def setup(n_sess, n, n_past):
+        pages = (n_past + n + 15) // 16
+        nb = int(pages.sum()) + 8
+        perm = rng.permutation(nb).astype(np.int32)
+        tables = np.zeros((n_sess, int(pages.max())), np.int32)
+        off = 0
+        for i in range(n_sess):
+            tables[i, :pages[i]] = perm[off:off + pages[i]]
+            off += pages[i]
+        pk, pv = nova.alloc(nb * nova.kb * nova.kvw * 2), nova.alloc(nb * nova.kb * nova.kvw * 2)
+        q = rng.standard_normal((n_sess, n, nh, hd)).astype(np.float32)
+        k = rng.standard_normal((n_sess, n, nkv, hd)).astype(np.float32)
+        v = rng.standard_normal((n_sess, n, nkv, hd)).astype(np.float32)
+        bufs = dict(q=nova.upload(q), k=nova.upload(k), v=nova.upload(v), t=nova.upload(tables),
+                    p=nova.upload(n_past.astype(np.int32)), pk=pk, pv=pv)
+        call = lambda: nova.launch_rope_kv_store_paged_batch(  # noqa: E731
+            bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr, cs.ptr, sn.ptr, pk.ptr, pv.ptr, bufs["t"].ptr,
+            tables.shape[1], bufs["p"].ptr, n_sess, n, 0, nb, s)
+        return call, (q, k, v, tables, nb, bufs)
+
+    def timed(call, steps):
+        for _ in range(args.warmup):
+            call()
+        t = Timer(nova, s)
+        t.start()
+        for _ in range(steps):
+            call()
+        return t.stop() / steps
+
+    n_past = rng.integers(0, 4097, 8).astype(np.int32)
+    chunk, (q, k, v, tables, nb, bufs) = setup(8, 512, n_past)
+    ms = timed(chunk, max(args.steps, 20))
+    nbytes = rope_bytes(8 * 512, nh, nkv, hd)
+    ctx = ragged_ctx(args.seed, 16, 512, 8192)
+    dec, _ = setup(16, 1, ctx)
+    dec_ms = timed(dec, max(args.steps, 50))
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    # parity of session 0's chunk against the oracle, on fresh inputs
+    from oracle_py import Oracle
+    orc = Oracle()
+    q0 = rng.standard_normal((8, 512, nh, hd)).astype(np.float32)
+    nova.dev_upload(bufs["q"].ptr, q0.ctypes.data, q0.nbytes)
+    chunk()
+    nova.dev_stream_sync(s)
+    hcs = nova.download(cs, (rows, hd // 2), np.float32)
+    hsn = nova.download(sn, (rows, hd // 2), np.float32)
+    got_q = nova.download(bufs["q"], q0.shape, np.float32)
+    shape = (nb, nova.kb, nkv, hd)
+    gk = nova.download(bufs["pk"], shape, np.uint16)
+    gv = nova.download(bufs["pv"], shape, np.uint16)
+    hk, hv = np.zeros(shape, np.uint16), np.zeros(shape, np.uint16)
+    t0 = time.perf_counter()
+    rq = orc.rope_kv_store_paged("qwen25_7b", q0[0], k[0], v[0], hcs, hsn, hk, hv,
+                                 np.ascontiguousarray(tables[0]), 0, nb, int(n_past[0]))
+    secs = time.perf_counter() - t0
+    rows0 = orc.kv_gather_paged("qwen25_7b", hk, tables[0], 0, nb, int(n_past[0]) + 512)[int(n_past[0]):]
+    got0 = orc.kv_gather_paged("qwen25_7b", gk, tables[0], 0, nb, int(n_past[0]) + 512)[int(n_past[0]):]
+    rv0 = orc.kv_gather_paged("qwen25_7b", hv, tables[0], 0, nb, int(n_past[0]) + 512)[int(n_past[0]):]
+    gv0 = orc.kv_gather_paged("qwen25_7b", gv, tables[0], 0, nb, int(n_past[0]) + 512)[int(n_past[0]):]
+    parity = bool(np.array_equal(got_q[0], rq) and np.array_equal(got0, rows0) and np.array_equal(gv0, rv0))
+    cpu_bytes = rope_bytes(512, nh, nkv, hd)
+    return {
+        "metric": "RoPE + paged fp16 append GB/s (config-5 chunk, Qwen2.5-7B)",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": max(args.steps, 20), "warmup": args.warmup,
+        "higher_is_better": True, "vs_baseline": None, "dtype": "f32 rotate / f16 store",
+        "data": "synthetic (seeded N(0,1) q, k, v; prefix U[0,4096]; seeded page shuffle)",
+        "config": {"workload": "8 sessions x 512-token chunk at n_past U[0,4096]: rotate q in place, rotate k "
+                               "and append k, v as fp16 through the block tables, one launch",
+                   "n_past": n_past.tolist(), "chunk": 512},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "rope_kernel<true> (launch_rope_kv_store_paged_batch)",
+                     "kernel_us": round(ms * 1e3, 2), "bytes_per_launch": nbytes},
+        "decode_step_us": round(dec_ms * 1e3, 2),
+        "decode_step": "16 sessions x 1 token (ctx U[512,8192]), one launch",
+        "parity": {"session0_q_k_v_bit_exact": parity},
+        "cpu_baseline": {"value": round(cpu_bytes / secs / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                         "sample": f"session 0's 512-token chunk, C oracle or_rope_kv_store_paged "
+                                   f"single-threaded, {secs * 1e3:.1f} ms"},
+    }
+
+
 def run_copycal(args):
     """Plain copy of 1 GiB (testkit_copy): the known-traffic kernel used to
     calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE (each launch reads and writes
@@ -590,6 +693,8 @@ def main():
         line = run_copycal(args)
     elif args.workload == "cow":
         line = run_cow(args)
+    elif args.workload == "rope":
+        line = run_rope(args)
     else:
         line = run_prefill(args)
     print(json.dumps(line), flush=True)

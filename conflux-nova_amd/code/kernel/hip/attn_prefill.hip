@@ -20,8 +20,8 @@
 //    barrier per tile.  The loop is unrolled by four so that every LDS
 //    operand address is a lane offset plus a compile-time constant.
 //    Rows keep their 256 B but the 16 B chunks are XOR-swizzled by row
-//    (chunk k of row r at position k ^ (r & 15)), so both operand reads below
-//    are free of LDS bank conflicts.
+//    (K: chunk k of row r at position k ^ (r & 15); V: k ^ 2 (r & 7)), so the
+//    operand reads below are free of LDS bank conflicts.
 //  * S^T = K . Q^T with v_mfma_f32_16x16x32_f16 (rows = 16 keys, cols = 16
 //    columns); every K operand read from LDS feeds both column blocks.  S^T's
 //    C layout is the B layout P^T needs, so O^T += V^T . P^T follows without
@@ -258,9 +258,17 @@ __device__ __forceinline__ u2 lds_read_tr(const unsigned char* p) {
     return __builtin_bit_cast(u2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(lp));
 }
 
-// byte offset of (row, chunk) inside a stage half (K or V)
-__device__ __forceinline__ uint32_t swz(int row, int chunk) {
+// Swizzles: the 16 B chunk k of tile row r sits at position k ^ f(r) of the
+// row.  K half: f(r) = r & 15 -- the score operand reads have the 16 lanes of
+// a group on 16 different rows at one chunk.  V half: f(r) = 2 (r & 7) -- the
+// transposing reads have each group on 4 consecutive rows at a chunk pair
+// (2cb, 2cb+1), and 8 consecutive rows must land on 16 distinct positions.
+// Both patterns are then free of bank conflicts.
+__device__ __forceinline__ uint32_t swz_k(int row, int chunk) {
     return (uint32_t)(row * ROWB + ((chunk ^ (row & 15)) << 4));
+}
+__device__ __forceinline__ uint32_t swz_v(int row, int chunk) {
+    return (uint32_t)(row * ROWB + ((chunk ^ (2 * (row & 7))) << 4));
 }
 
 // two workgroups per CU (<= 256 registers per wave): while one wave runs its
@@ -307,16 +315,19 @@ prefill_kernel(PrefillArgs a) {
     // ---- staging ----
     // Stage chunk q = tid + THREADS*u (u = 0..3): K for u < 2, V for u >= 2;
     // page u & 1 of the tile; row (tid >> 4) of that page; LDS position
-    // tid & 15 of the row holds global chunk (tid & 15) ^ (tid >> 4).  So a
-    // lane's offset inside a page is the same for all four loads, and each
-    // load instruction of a wave covers 4 rows of one page (wave-uniform base).
+    // tid & 15 of the row holds global chunk (tid & 15) ^ f(tid >> 4), with the
+    // K or V swizzle f.  So a lane's offset inside a page is one of two values
+    // for all four loads, and each load instruction of a wave covers 4 rows of
+    // one page (wave-uniform base).
     const char* pk = reinterpret_cast<const char*>(a.pool_k);
     const char* pv = reinterpret_cast<const char*>(a.pool_v);
     const int64_t layer_page0 = (int64_t)a.layer * a.nb;
     const int n_pages = (key_end + kKvBlock - 1) >> kKvBlockShift;
     const int srow = tid >> 4;                               // row inside the page
-    const int schunk = (tid & 15) ^ srow;                    // global chunk this lane moves
-    const uint32_t loff = (uint32_t)(srow * (KVW * 2) + 16 * schunk);
+    const int schunk_k = (tid & 15) ^ srow;                  // global chunk this lane moves (K, V)
+    const int schunk_v = (tid & 15) ^ (2 * (srow & 7));
+    const uint32_t loff_k = (uint32_t)(srow * (KVW * 2) + 16 * schunk_k);
+    const uint32_t loff_v = (uint32_t)(srow * (KVW * 2) + 16 * schunk_v);
     const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);
     int win0 = 0;                                            // first page of the LDS table window
     auto load_window = [&](int first) {                      // every thread, uniform
@@ -346,18 +357,19 @@ prefill_kernel(PrefillArgs a) {
         if (TILE * (T + 1) <= key_end) {
 #pragma unroll
             for (int u = 0; u < LOADS; ++u)
-                dma16((u < 2 ? pk : pv) + ((u & 1) ? b1 : b0) + loff, m0base + 16u * THREADS * u);
+                dma16((u < 2 ? pk + loff_k : pv + loff_v) + ((u & 1) ? b1 : b0), m0base + 16u * THREADS * u);
         } else {
             // the tile holding the last key: rows past it (never written, may
             // hold NaN bits) load the last key's row instead; their weights are
             // masked to zero
             const int rl = key_end - 1 - TILE * T;           // in [0, TILE)
-            const int64_t bl = ((rl >> 4) ? b1 : b0) + (int64_t)((rl & 15) * (KVW * 2) + 16 * schunk);
+            const int64_t bl = ((rl >> 4) ? b1 : b0) + (int64_t)(rl & 15) * (KVW * 2);
 #pragma unroll
             for (int u = 0; u < LOADS; ++u) {
                 const int row = srow + 16 * (u & 1);
-                const char* pool = u < 2 ? pk : pv;
-                dma16(TILE * T + row < key_end ? pool + ((u & 1) ? b1 : b0) + loff : pool + bl,
+                const char* pool = u < 2 ? pk + 16 * schunk_k : pv + 16 * schunk_v;
+                const int64_t rowoff = (int64_t)srow * (KVW * 2);
+                dma16(TILE * T + row < key_end ? pool + ((u & 1) ? b1 : b0) + rowoff : pool + bl,
                       m0base + 16u * THREADS * u);
             }
         }
@@ -417,12 +429,12 @@ prefill_kernel(PrefillArgs a) {
     // 16cb + 4 (s & 3) .. +3 of it
     uint32_t koff[4], voff[8];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) koff[ks] = swz(c, 4 * ks + g);
+    for (int ks = 0; ks < 4; ++ks) koff[ks] = swz_k(c, 4 * ks + g);
     {
         const int vr = 4 * g + (c >> 2);
         const int vh = (c >> 1) & 1;
 #pragma unroll
-        for (int cb = 0; cb < 8; ++cb) voff[cb] = TILE * ROWB + swz(vr, 2 * cb + vh) + 8 * (c & 1);
+        for (int cb = 0; cb < 8; ++cb) voff[cb] = TILE * ROWB + swz_v(vr, 2 * cb + vh) + 8 * (c & 1);
     }
 
     // tiles 0 and 1 resident (tile 2 may still be loading)

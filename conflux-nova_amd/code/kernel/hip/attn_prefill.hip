@@ -498,11 +498,18 @@ prefill_kernel(PrefillArgs a) {
             for (int j = 0; j < 8; ++j) v = ok[b][j] ? fmaxf(v, x[b][j]) : v;
             lmax[b] = v;
         }
-        // score MFMAs of the next tile interleaved with the tests above
+        // the weights, assuming no column's max moves (recomputed below if one
+        // does): computed here so that they overlap the next tile's MFMAs
+        h8 ph[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ph[b][j] = (_Float16)(ok[b][j] ? __builtin_amdgcn_exp2f(x[b][j]) : 0.f);
+        // score MFMAs of the next tile interleaved with the work above
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);   // one VALU
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
         }
         if (__builtin_amdgcn_ballot_w64(lmax[0] > kLazy || lmax[1] > kLazy) || key_base == 0) {
             // rare (and the first tile): move the max of every column whose
@@ -519,18 +526,15 @@ prefill_kernel(PrefillArgs a) {
                 for (int cb = 0; cb < 8; ++cb) acc[b][cb] *= corr;
                 m[b] += shift;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) x[b][j] -= shift;
+                for (int j = 0; j < 8; ++j)
+                    ph[b][j] = (_Float16)(ok[b][j] ? __builtin_amdgcn_exp2f(x[b][j] - shift) : 0.f);
                 n0[b] -= shift;                  // the next tile's scores were seeded with the old max
                 n1[b] -= shift;
                 negm[b] = f4{-m[b], -m[b], -m[b], -m[b]};
             }
         }
-        h8 ph[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-                ph[b][j] = (_Float16)(ok[b][j] ? __builtin_amdgcn_exp2f(x[b][j]) : 0.f);
             // l += ones . P^T: the sum of exactly the fp16 weights applied below
             lsum[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph[b], lsum[b], 0, 0, 0);
 #pragma unroll

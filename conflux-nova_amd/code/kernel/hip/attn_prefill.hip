@@ -533,6 +533,7 @@ prefill_kernel(PrefillArgs a) {
                 negm[b] = f4{-m[b], -m[b], -m[b], -m[b]};
             }
         }
+        __builtin_amdgcn_s_setprio(1);   // the PV MFMAs go first on the SIMD
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             // l += ones . P^T: the sum of exactly the fp16 weights applied below
@@ -541,6 +542,7 @@ prefill_kernel(PrefillArgs a) {
             for (int cb = 0; cb < 8; ++cb)
                 acc[b][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[cb], ph[b], acc[b][cb], 0, 0, 0);
         }
+        __builtin_amdgcn_s_setprio(0);
     };
 
     // Tile pipeline over NBUF = 4 buffers.  Step t (buffer t % 4): issue the

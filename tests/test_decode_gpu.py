@@ -155,3 +155,29 @@ def test_decode_plan_reused_across_layers(nova7, oracle):
             ref = oracle.attn_decode_paged("qwen25_7b", np.ascontiguousarray(q[i]), hk, hv, tables[i], 0, nb,
                                            int(n_keys[i]))
             assert_close(got[i], ref, what=f"layer {layer} session {i}")
+
+
+def test_decode_batch_many_sessions(nova7, oracle):
+    """300 ragged sessions (some empty): more sessions than one wave's 64-lane
+    passes over the batch and than the 256-workgroup grid base."""
+    nova = nova7
+    rng = np.random.default_rng(31)
+    n_sess = 300
+    n_keys = rng.integers(0, 300, n_sess).astype(np.int32)
+    n_keys[::37] = 0
+    n_keys[5] = 1
+    max_pages = int((n_keys.max() + 15) // 16)
+    print(f"[case] decode batch n_sess={n_sess}", flush=True)
+    fx = PagedFixture(nova, nb=n_sess * max_pages + 3, layer=LAYER, seed=31)
+    tables = fx.tables(n_sess, max_pages)
+    q = rng.standard_normal((n_sess, nova.nh, nova.hd)).astype(np.float32)
+    got = _batch(nova, fx, q, tables, n_keys)
+    worst = 0.0
+    for i in range(n_sess):
+        if n_keys[i] == 0:
+            assert (got[i] == 0).all(), i
+            continue
+        ref = oracle.attn_decode_paged("qwen25_7b", np.ascontiguousarray(q[i]), fx.hk, fx.hv, tables[i], 0, fx.nb,
+                                       int(n_keys[i]))
+        worst = max(worst, assert_close(got[i], ref, what=f"session {i} n_keys={n_keys[i]}"))
+    print(f"  worst max|gpu-oracle|={worst:.3e}")

@@ -132,3 +132,30 @@ def test_prefill_sharp_scores(scale, n_q, n_past, nova7, oracle):
     ref = oracle.attn_prefill_paged("qwen25_7b", q, fx.hk, fx.hv, table, 0, fx.nb, n_q, n_past)
     err = assert_close(got, ref, what=f"sharp scale={scale} n_q={n_q} n_past={n_past}")
     print(f"  max|gpu-oracle|={err:.3e}")
+
+
+def test_prefill_batch_beyond_ranking(nova7, oracle):
+    """250 sessions x 300 queries = 4250 (session, column group) items: past the
+    in-kernel ranking limit, so workgroups take items in natural order.  Every
+    output row must be written (the output starts as NaN); sampled sessions are
+    checked against the oracle."""
+    nova = nova7
+    rng = np.random.default_rng(41)
+    n, n_q = 250, 300
+    n_past = rng.integers(0, 41, n).astype(np.int32)
+    print(f"[case] prefill batch n_sess={n} n_q={n_q}", flush=True)
+    pages = int((n_past.max() + n_q + 15) // 16)
+    fx = PagedFixture(nova, nb=n * pages + 2, layer=LAYER, seed=41)
+    tables = fx.tables(n, pages)
+    q = rng.standard_normal((n, n_q, nova.nh, nova.hd)).astype(np.float32)
+    dq, dt, dn = nova.upload(q), nova.upload(tables), nova.upload(n_past)
+    do = nova.upload(np.full(q.shape, np.nan, np.float32))
+    nova.launch_attn_prefill_paged_batch(dq.ptr, fx.k.ptr, fx.v.ptr, dt.ptr, pages, dn.ptr, n, n_q, LAYER, fx.nb,
+                                         do.ptr, None)
+    nova.dev_sync()
+    got = do.numpy(q.shape, np.float32)
+    assert np.all(np.isfinite(got))
+    for i in (0, 97, 173, 249):
+        ref = oracle.attn_prefill_paged("qwen25_7b", np.ascontiguousarray(q[i]), fx.hk, fx.hv, tables[i], 0, fx.nb,
+                                        n_q, int(n_past[i]))
+        assert_close(got[i], ref, what=f"session {i}")

@@ -422,8 +422,8 @@ decode_split_kernel(DecodeArgs a) {
         };
 
         // each wave keeps one pair (16 KiB) in flight; the 8 waves of the CU
-        // overlap each other's latency (a register ping-pong of two pairs does
-        // not fit the 256-VGPR budget of 2 waves per SIMD without spilling)
+        // overlap each other's latency (measured: a register ping-pong of two
+        // pairs per wave, with Q re-read from LDS to fit 256 VGPRs, is slower)
         for (int qp = r; qp < npairs; qp += R) {
             if (qp != r || !early) load_pair(qp, cur);
             compute_pair(qp, cur);

@@ -44,10 +44,14 @@
 //    MFMAs start from -m (accumulator seed), so they yield s - m directly; the
 //    common case is one lane-local comparison against 8 and a wave ballot,
 //    and only a rescale takes the row max across the four 16-lane rows
-//    (v_permlane16/32_swap, no LDS round trip).  Exponentials use the raw
-//    v_exp_f32; tiles wholly below the causal diagonal run a mask-free path.
-//  * The workgroup's slice of the block table sits in LDS (windows of 4096
-//    pages), so a page lookup never waits on the vector-memory counter that
+//    (v_permlane16/32_swap, no LDS round trip) and corrects the next tile's
+//    already-issued scores by the same shift.  The weights are computed before
+//    that (rare) branch, assuming no max moves, so the exponentials overlap the
+//    next tile's score MFMAs; the PV MFMA burst runs at raised wave priority.
+//    Exponentials use the raw v_exp_f32; tiles wholly below the causal
+//    diagonal run a mask-free path.
+//  * The workgroup's slice of the block table sits in LDS (windows of 2048
+//    pages), read a tile ahead, so a page lookup never waits on the vector-memory counter that
 //    the tile loads in flight occupy; causal masking is per (key, column);
 //    tiles past the workgroup's last query are never visited.
 //  * Scheduling.  A work item is (session, column group); its cost is its

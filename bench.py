@@ -518,6 +518,14 @@ def run_prefill(args):
                                              o.ptr + l * q_h.nbytes, s)
         tot += t.stop()
     k_ms = tot / L
+    # the reference's call pattern: one launch_attn_prefill_paged per session
+    t.start()
+    for l in range(L):
+        for i in range(n_sess):
+            nova.launch_attn_prefill_paged(q.ptr + i * n_q * nova.nh * nova.hd * 4, k.ptr, v.ptr,
+                                           dt.ptr + i * stride * 4, l, nb, n_q, int(n_past[i]),
+                                           o.ptr + l * q_h.nbytes + i * n_q * nova.nh * nova.hd * 4, s)
+    single_ms = t.stop() / L
     flops = prefill_flops(n_past, n_q, nova.nh, nova.hd)
     tflops = flops / (k_ms * 1e-3) / 1e12
     cpu = None
@@ -546,6 +554,10 @@ def run_prefill(args):
         "dtype": "f16 MFMA / f32 accumulate", "data": "synthetic (seeded N(0,1) Q/K/V, prefix U[0,4096])",
         "config": {"workload": "config5: 8 sessions, 512-token chunk appended then causal attention over "
                                "prefix U[0,4096] + chunk, 28 layers", "n_past": n_past.tolist(), "chunk": n_q},
+        "per_session_launches": {"us_per_layer": round(single_ms * 1e3, 2),
+                                 "tflops": round(flops / (single_ms * 1e-3) / 1e12, 2),
+                                 "what": "the same layer as 8 launch_attn_prefill_paged calls (the reference's "
+                                         "one-session-per-call pattern, src/model.cpp AttnOp)"},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / FP16_MFMA_PEAK_TFLOPS, 4), "traffic": load_traffic("prefill"),
                      "kernel": "prefill_kernel (launch_attn_prefill_paged_batch)",

@@ -8,11 +8,12 @@
 // streams every key once per query; here the work is a dense contraction:
 //
 //  * Columns.  For one kv head the chunk has n_q*G (query, head) pairs, all
-//    needing the same K/V rows.  A wave owns NB = 2 blocks of 16 such columns
-//    (col = qi*G + hh); a workgroup of 4 waves owns 128 consecutive columns of
-//    one (session, kv head); two workgroups share a CU (2 waves per SIMD, so
-//    one wave's softmax overlaps the other's MFMAs; measured 1.5x over one
-//    wave per SIMD with 4 blocks).
+//    needing the same K/V rows.  A wave owns NB blocks of 16 such columns
+//    (col = qi*G + hh); a workgroup of 4 waves owns 64*NB consecutive columns
+//    of one (session, kv head); two workgroups share a CU (2 waves per SIMD, so
+//    one wave's softmax overlaps the other's MFMAs).  NB = 2 when the launch
+//    has enough (session, column group) items to fill the chip, NB = 1 (twice
+//    the workgroups) for small launches such as one session's chunk.
 //  * K/V tiles of 32 keys (2 pages) are staged ONCE per workgroup in LDS by
 //    direct global->LDS loads (global_load_lds_dwordx4: no staging
 //    registers), four buffers: while tile t's softmax runs, the scores of
@@ -83,9 +84,6 @@ constexpr int NH = Model::NH, NKV = Model::NKV, HD = Model::HD, G = Model::G, KV
 constexpr int NBUF = 4;                        // K/V tile buffers in LDS
 constexpr int WAVES = 4;
 constexpr int THREADS = WAVES * 64;
-constexpr int NB = 2;                          // 16-column blocks per wave
-constexpr int COLS_WAVE = 16 * NB;
-constexpr int COLS_WG = COLS_WAVE * WAVES;
 constexpr int TILE = 32;                       // keys per stage (2 pages)
 constexpr int ROWB = HD * 2;                   // 256 B per K or V row of one kv head
 constexpr int STAGE_BYTES = 2 * TILE * ROWB;   // K then V
@@ -124,9 +122,9 @@ __device__ __forceinline__ int n_past_of(const PrefillArgs& a, int sess) {
 }
 
 // cost (key tiles) of item j = sess * n_cg + cg, clamped to the histogram
-__device__ __forceinline__ int item_bucket(const PrefillArgs& a, int j, int n_cg, int n_cols) {
+__device__ __forceinline__ int item_bucket(const PrefillArgs& a, int j, int n_cg, int n_cols, int cols_wg) {
     const int sess = j / n_cg, cg = j - sess * n_cg;
-    const int last_col = min(cg * COLS_WG + COLS_WG, n_cols) - 1;
+    const int last_col = min(cg * cols_wg + cols_wg, n_cols) - 1;
     const int key_end = n_past_of(a, sess) + last_col / G + 1;
     return min((key_end + TILE - 1) / TILE, kBuckets - 1);
 }
@@ -134,7 +132,7 @@ __device__ __forceinline__ int item_bucket(const PrefillArgs& a, int j, int n_cg
 // The item of rank r in decreasing cost order (ties in index order).  Every
 // thread of the workgroup calls it (it has barriers) and gets the same answer.
 // s_i: LDS scratch of kBuckets + THREADS + 16 ints.
-__device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int* s_i) {
+__device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int cols_wg, int* s_i) {
     const int N = a.n_sess * n_cg;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int* hist = s_i;
@@ -142,7 +140,7 @@ __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int* 
     int* res = part + THREADS;          // [0] group, [1] ranks above it, [2] item, [4..] wave counts
     for (int b = tid; b < kBuckets; b += THREADS) hist[b] = 0;
     __syncthreads();
-    for (int j = tid; j < N; j += THREADS) atomicAdd(&hist[item_bucket(a, j, n_cg, n_cols)], 1);
+    for (int j = tid; j < N; j += THREADS) atomicAdd(&hist[item_bucket(a, j, n_cg, n_cols, cols_wg)], 1);
     __syncthreads();
     constexpr int PER = kBuckets / THREADS;
     int sum = 0;
@@ -187,7 +185,7 @@ __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int* 
     // the o-th item (index order) whose cost falls in that bucket
     for (int j0 = 0; j0 < N; j0 += THREADS) {
         const int j = j0 + tid;
-        const bool f = j < N && item_bucket(a, j, n_cg, n_cols) == bucket;
+        const bool f = j < N && item_bucket(a, j, n_cg, n_cols, cols_wg) == bucket;
         const uint64_t bal = __builtin_amdgcn_ballot_w64(f);
         if (lane == 0) res[4 + wave] = __builtin_popcountll(bal);
         __syncthreads();
@@ -277,8 +275,11 @@ __device__ __forceinline__ uint32_t swz_v(int row, int chunk) {
 
 // two workgroups per CU (<= 256 registers per wave): while one wave runs its
 // softmax on the VALU the other wave of the SIMD keeps the matrix core busy
+template <int NB>                                // 16-column blocks per wave
 __global__ void __launch_bounds__(THREADS, 2)   // 2 waves per SIMD: <= 256 VGPRs
 prefill_kernel(PrefillArgs a) {
+    constexpr int COLS_WAVE = 16 * NB;
+    constexpr int COLS_WG = COLS_WAVE * WAVES;
     __shared__ __attribute__((aligned(16))) unsigned char s_kv[NBUF][STAGE_BYTES];
     __shared__ int32_t s_tab[kTabWin];
     static_assert((kBuckets + THREADS + 16) * 4 <= (int)sizeof(s_kv), "ranking scratch fits the tile buffers");
@@ -299,7 +300,7 @@ prefill_kernel(PrefillArgs a) {
     if (rank >= N) return;                                  // grid padding (uniform)
     int item;
     if (a.n_sess == 1 || N > kRankMax) item = (rank / n_cg) * n_cg + (n_cg - 1 - rank % n_cg);
-    else item = lpt_item(a, rank, n_cg, n_cols, reinterpret_cast<int*>(&s_kv[0][0]));
+    else item = lpt_item(a, rank, n_cg, n_cols, COLS_WG, reinterpret_cast<int*>(&s_kv[0][0]));
     const int sess = item / n_cg;
     const int cg = item - sess * n_cg;
     const int n_past = n_past_of(a, sess);
@@ -511,11 +512,14 @@ prefill_kernel(PrefillArgs a) {
             for (int j = 0; j < 8; ++j) ph[b][j] = (_Float16)(ok[b][j] ? __builtin_amdgcn_exp2f(x[b][j]) : 0.f);
         // score MFMAs of the next tile interleaved with the work above
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
+        for (int i = 0; i < 8 * NB; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
             __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
         }
-        if (__builtin_amdgcn_ballot_w64(lmax[0] > kLazy || lmax[1] > kLazy) || key_base == 0) {
+        bool over = false;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) over |= lmax[b] > kLazy;
+        if (__builtin_amdgcn_ballot_w64(over) || key_base == 0) {
             // rare (and the first tile): move the max of every column whose
             // tile max exceeds it by more than kLazy.  bm = -inf: no key of the
             // column in this tile, nothing moves.
@@ -599,11 +603,29 @@ prefill_kernel(PrefillArgs a) {
     }
 }
 
+int compute_units() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        NOVA_HIP(hipGetDevice(&dev));
+        NOVA_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    }
+    return cus;
+}
+
+// Column groups of 128 (2 blocks per wave) when the launch has enough work
+// items to fill two workgroups per CU; otherwise of 64 (1 block per wave):
+// twice the workgroups for a single session's chunk, each with half the
+// columns (same key tiles, half the work per tile).
 void launch(const PrefillArgs& a, int n_sess, hipStream_t s) {
-    const int64_t n_cg = (a.n_q * G + COLS_WG - 1) / COLS_WG;
+    const int64_t items128 = (a.n_q * G + 127) / 128 * (int64_t)n_sess * NKV;
+    const bool wide = items128 >= 2 * (int64_t)compute_units();
+    const int cols_wg = wide ? 128 : 64;
+    const int64_t n_cg = (a.n_q * G + cols_wg - 1) / cols_wg;
     const int64_t n_wg = (n_cg * n_sess * NKV + kXcd - 1) / kXcd * kXcd;
     NOVA_REQUIRE(n_wg < (int64_t)1 << 31);
-    hipLaunchKernelGGL(prefill_kernel, dim3((unsigned)n_wg), dim3(THREADS), 0, s, a);
+    if (wide) hipLaunchKernelGGL(prefill_kernel<2>, dim3((unsigned)n_wg), dim3(THREADS), 0, s, a);
+    else hipLaunchKernelGGL(prefill_kernel<1>, dim3((unsigned)n_wg), dim3(THREADS), 0, s, a);
     NOVA_LAUNCHED();
 }
 

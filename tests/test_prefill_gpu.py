@@ -159,3 +159,28 @@ def test_prefill_batch_beyond_ranking(nova7, oracle):
         ref = oracle.attn_prefill_paged("qwen25_7b", np.ascontiguousarray(q[i]), fx.hk, fx.hv, tables[i], 0, fx.nb,
                                         n_q, int(n_past[i]))
         assert_close(got[i], ref, what=f"session {i}")
+
+
+def test_prefill_batch_wide_ranked(nova7, oracle):
+    """8 sessions x 512 queries: enough (session, column group) items for the
+    128-column workgroups, taken in ranked (longest-first) order."""
+    nova = nova7
+    n_past = np.array([0, 5, 100, 37, 250, 16, 17, 64], np.int32)
+    n, n_q = len(n_past), 512
+    print(f"[case] prefill batch wide n_past={n_past.tolist()}", flush=True)
+    pages = int((n_past.max() + n_q + 15) // 16)
+    fx = PagedFixture(nova, nb=n * pages + 2, layer=LAYER, seed=55)
+    tables = fx.tables(n, pages)
+    q = fx.rng.standard_normal((n, n_q, nova.nh, nova.hd)).astype(np.float32)
+    dq, dt, dn = nova.upload(q), nova.upload(tables), nova.upload(n_past)
+    do = nova.upload(np.full(q.shape, np.nan, np.float32))
+    nova.launch_attn_prefill_paged_batch(dq.ptr, fx.k.ptr, fx.v.ptr, dt.ptr, pages, dn.ptr, n, n_q, LAYER, fx.nb,
+                                         do.ptr, None)
+    nova.dev_sync()
+    got = do.numpy(q.shape, np.float32)
+    assert np.all(np.isfinite(got))
+    for i in (0, 4, 7):
+        ref = oracle.attn_prefill_paged("qwen25_7b", np.ascontiguousarray(q[i]), fx.hk, fx.hv, tables[i], 0, fx.nb,
+                                        n_q, int(n_past[i]))
+        err = assert_close(got[i], ref, what=f"session {i}")
+        print(f"  session {i} max|gpu-oracle|={err:.3e}")

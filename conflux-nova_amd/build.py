@@ -36,6 +36,7 @@ HIP_SOURCES = [
     "code/kernel/hip/attn_prefill.hip",
     "code/kernel/hip/kv_pages.hip",
     "code/kernel/hip/rope.hip",
+    "code/kernel/hip/q4k.hip",
     "code/kernel/hip/testkit.hip",
 ]
 CXX_SOURCES = [

@@ -74,6 +74,8 @@ _SIGS = {
     "launch_attn_decode_paged_planned": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]),
     "launch_attn_prefill_paged_batch": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp]),
     "launch_kv_store_paged_batch": (None, [vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp]),
+    "launch_quant_q8": (None, [vp, vp, vp, vp, i32, i32, vp]),
+    "launch_gemv_q4k": (None, [vp, i64, i32, vp, vp, vp, vp, vp]),
     "launch_rope_table": (None, [vp, vp, vp]),
     "launch_rope_table_rows": (None, [vp, vp, i32, vp]),
     "launch_rope_batch": (None, [vp, vp, i32, i64, vp, vp, vp]),

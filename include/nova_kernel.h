@@ -168,6 +168,23 @@ void launch_rope_kv_store_paged_batch(float* q, const float* k, const float* v, 
                                       const int32_t* tables, int table_stride, const int32_t* n_past,
                                       int n_sess, int n, int layer, int nb, nova_stream_t s);
 
+/* ---- Q4_K GEMV (src/kernel/q4k_gemv.cu), weights in ggml block_q4_K
+ * (include/nova/quant/q4_k.h:19-25: 144 B per 256 weights, row-major,
+ * rows x cols/256 blocks), activations as ActQ8 (include/nova/kernel/types.h:24-28)
+ * passed as three plain arrays: int8 codes [rows][cols], fp32 scales
+ * [rows][cols/32], int32 sums of each 16 codes [rows][cols/16]. ---- */
+
+/* Quantise rows x cols fp32 activations (cols % 32 == 0).  Replaces
+ * nova::launch_quant / launch_quant_ffn, q4k_gemv.cu:196-207 (kernel :9-33),
+ * which fix cols to D or FFN at compile time. */
+void launch_quant_q8(int8_t* qs, float* d, int32_t* sums, const float* x, int rows, int cols, nova_stream_t s);
+/* out[r] = row r of the Q4_K matrix . the quantised activation (one token),
+ * cols % 256 == 0, cols <= 32768.  Replaces nova::launch_gemv<K, R>,
+ * q4k_gemv.cu:209-213 (kernel :35-91; Q4KWeight = {blocks, rows, cols},
+ * types.h:17-21, passed here as plain arguments). */
+void launch_gemv_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_t* xq, const float* xd,
+                     const int32_t* xs, float* out, nova_stream_t s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -470,6 +470,88 @@ void or_rope_kv_store_paged(or_geom g, float* q, const float* k, const float* v,
     free(kr);
 }
 
+/* ---- Q4_K ---- */
+float or_q4k_half(uint16_t h) {
+    /* half_to_float q4_k.h:28-41 (host branch) */
+    const int sgn = (h >> 15) & 1, e = (h >> 10) & 0x1F;
+    const uint32_t m = h & 0x3FFu;
+    double v;
+    if (e == 0) v = ldexp((double)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = ldexp((double)(m | 0x400u), e - 25);
+    return (float)(sgn ? -v : v);
+}
+
+static void q4k_scale_min(int j, const uint8_t* q, uint8_t* sc, uint8_t* m) {
+    /* get_scale_min_k4 q4_k.h:44-52 */
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+void or_q4k_dequant_block(const uint8_t* block, float* y) {
+    /* dequant_block q4_k.h:55-73: sub-block 2g from the low nibbles of
+       qs[32g..32g+31], 2g+1 from the high nibbles */
+    uint16_t hd, hm;
+    memcpy(&hd, block, 2);
+    memcpy(&hm, block + 2, 2);
+    const float d = or_q4k_half(hd), dmin = or_q4k_half(hm);
+    const uint8_t* scales = block + 4;
+    const uint8_t* q = block + 16;
+    for (int g = 0; g < 4; ++g) {
+        uint8_t sc0, m0, sc1, m1;
+        q4k_scale_min(2 * g, scales, &sc0, &m0);
+        q4k_scale_min(2 * g + 1, scales, &sc1, &m1);
+        const float d0 = d * (float)sc0, e0 = dmin * (float)m0;
+        const float d1 = d * (float)sc1, e1 = dmin * (float)m1;
+        for (int l = 0; l < 32; ++l) y[g * 64 + l] = d0 * (float)(q[32 * g + l] & 0xF) - e0;
+        for (int l = 0; l < 32; ++l) y[g * 64 + 32 + l] = d1 * (float)(q[32 * g + l] >> 4) - e1;
+    }
+}
+
+void or_quant_q8(const float* x, int rows, int cols, int8_t* qs, float* d, int32_t* s) {
+    /* quant_kernel q4k_gemv.cu:9-33 */
+    for (int r = 0; r < rows; ++r) {
+        for (int b = 0; b < cols / 32; ++b) {
+            const float* xp = x + (int64_t)r * cols + 32 * b;
+            float amax = 0.f;
+            for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(xp[i]));
+            const float scale = amax * (1.f / 127.f);
+            const float inv = amax > 0.f ? 127.f / amax : 0.f;
+            int s0 = 0, s1 = 0;
+            for (int i = 0; i < 32; ++i) {
+                const int v = (int)rintf(xp[i] * inv);
+                qs[(int64_t)r * cols + 32 * b + i] = (int8_t)v;
+                if (i < 16) s0 += v; else s1 += v;
+            }
+            d[(int64_t)r * (cols / 32) + b] = scale;
+            s[(int64_t)r * (cols / 16) + 2 * b] = s0;
+            s[(int64_t)r * (cols / 16) + 2 * b + 1] = s1;
+        }
+    }
+}
+
+void or_gemv_q4k(const uint8_t* w, int64_t rows, int64_t cols, const int8_t* qs, const float* d,
+                 const int32_t* s, double* out) {
+    (void)s;
+    float y[256];
+    for (int64_t r = 0; r < rows; ++r) {
+        double acc = 0.0;
+        for (int64_t b = 0; b < cols / 256; ++b) {
+            or_q4k_dequant_block(w + (r * (cols / 256) + b) * 144, y);
+            for (int i = 0; i < 256; ++i) {
+                const int64_t k = 256 * b + i;
+                acc += (double)y[i] * ((double)qs[k] * (double)d[k / 32]);
+            }
+        }
+        out[r] = acc;
+    }
+}
+
 void or_kv_gather_paged(or_geom g, const uint16_t* pool, const int32_t* table, int layer, int nb,
                         int64_t n, uint16_t* out) {
     const int64_t kvw = (int64_t)g.nkv * g.hd;

@@ -107,6 +107,20 @@ void or_rope_kv_store_paged(or_geom g, float* q, const float* k, const float* v,
                             const float* sn, uint16_t* pool_k, uint16_t* pool_v, const int32_t* table,
                             int layer, int nb, int n, int64_t pos0);
 
+/* ---------------- Q4_K GEMV (src/kernel/q4k_gemv.cu, include/nova/quant/q4_k.h) ----------------
+ * Weights: rows x (cols/256) ggml block_q4_K (144 B: fp16 d, fp16 dmin,
+ * 12 B of packed 6-bit (scale, min) for 8 sub-blocks of 32, 128 B of nibbles;
+ * q4_k.h:19-25).  Activations ActQ8 (include/nova/kernel/types.h:24-28): per
+ * row int8 qs[cols], float d[cols/32], int s[cols/16] (sum of each 16 int8). */
+float or_q4k_half(uint16_t h);                                            /* q4_k.h:28-41 */
+void  or_q4k_dequant_block(const uint8_t* block, float* y);              /* q4_k.h:55-73 */
+/* quant_kernel q4k_gemv.cu:9-33: amax over 32, d = amax/127, q = rint(x*127/amax) */
+void  or_quant_q8(const float* x, int rows, int cols, int8_t* qs, float* d, int32_t* s);
+/* out[r] = sum_b dot(dequant(w[r]), x_q * x_d) in double: the value the GEMV
+ * (gemv_kernel q4k_gemv.cu:35-91) computes in fp32 with its own order */
+void  or_gemv_q4k(const uint8_t* w, int64_t rows, int64_t cols, const int8_t* qs, const float* d,
+                  const int32_t* s, double* out);
+
 /* ---------------- COW page copy (src/model.cpp:171-191) ---------------- */
 void or_cow_copy(or_geom g, uint16_t* pool_k, uint16_t* pool_v, int n_layers, int nb,
                  int src, int dst);

@@ -122,6 +122,10 @@ class Oracle:
         L.or_attn_prefill_paged_f64.argtypes = [Geom, vp, vp, vp, vp, i32, i32, i32, i32, vp]
         L.or_attn_decode_batch.argtypes = [Geom, vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, i32]
         L.or_rope_table.argtypes = [vp, vp, i32, i32, C.c_double]
+        L.or_q4k_half.restype, L.or_q4k_half.argtypes = C.c_float, [C.c_uint16]
+        L.or_q4k_dequant_block.argtypes = [vp, vp]
+        L.or_quant_q8.argtypes = [vp, i32, i32, vp, vp, vp]
+        L.or_gemv_q4k.argtypes = [vp, i64, i64, vp, vp, vp, vp]
         L.or_rope_apply.argtypes = [Geom, vp, vp, i32, i64, vp, vp]
         L.or_rope_kv_store_paged.argtypes = [Geom, vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i64]
 
@@ -172,6 +176,31 @@ class Oracle:
            self._p(out))
         return out
 
+    # ---- Q4_K ----
+    def q4k_half(self, h: int) -> float:
+        return self.lib.or_q4k_half(h)
+
+    def q4k_dequant_block(self, block: np.ndarray) -> np.ndarray:
+        block = np.ascontiguousarray(block, np.uint8)
+        y = np.empty(256, np.float32)
+        self.lib.or_q4k_dequant_block(self._p(block), self._p(y))
+        return y
+
+    def quant_q8(self, x: np.ndarray):
+        x = np.ascontiguousarray(x, np.float32)
+        rows, cols = x.shape
+        qs = np.empty((rows, cols), np.int8)
+        d = np.empty((rows, cols // 32), np.float32)
+        s = np.empty((rows, cols // 16), np.int32)
+        self.lib.or_quant_q8(self._p(x), rows, cols, self._p(qs), self._p(d), self._p(s))
+        return qs, d, s
+
+    def gemv_q4k(self, w: np.ndarray, rows: int, cols: int, qs, d, s) -> np.ndarray:
+        out = np.empty(rows, np.float64)
+        self.lib.or_gemv_q4k(self._p(np.ascontiguousarray(w, np.uint8)), rows, cols, self._p(qs), self._p(d),
+                             self._p(s), self._p(out))
+        return out
+
     # ---- RoPE ----
     def rope_table(self, rows, half=64, theta=1e6):
         cs = np.empty((rows, half), np.float32)
@@ -218,6 +247,13 @@ class Reference:
         L.ref_kv_hash_ids.restype, L.ref_kv_hash_ids.argtypes = u64, [P_int, sz]
         L.ref_kv_hash_text.restype, L.ref_kv_hash_text.argtypes = u64, [C.c_char_p, sz]
         L.ref_kv_block_id.restype, L.ref_kv_block_id.argtypes = None, [u64, u64, C.c_char_p]
+        self.q4k = None
+        p = REF_DIR / "libnova_ref_q4k.so"
+        if p.exists():
+            self.q4k = C.CDLL(str(p))
+            self.q4k.ref_q4k_half.restype, self.q4k.ref_q4k_half.argtypes = C.c_float, [C.c_uint16]
+            self.q4k.ref_q4k_dequant_block.argtypes = [vp, vp]
+            self.q4k.ref_q4k_selftest_block.argtypes = [vp]
         self.attn = {}
         for model, tag in (("qwen25_7b", "7b"), ("qwen25_1p5b", "1p5b")):
             p = REF_DIR / f"libnova_ref_attn_{tag}.so"

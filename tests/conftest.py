@@ -19,6 +19,14 @@ def oracle():
     return Oracle()
 
 
+@pytest.fixture(scope="session")
+def reference():
+    """The reference's own code built into oracle/_ref (None where the
+    reference tree was absent at build time, e.g. on the GPU box)."""
+    from oracle_py import Reference
+    return Reference() if Reference.available() else None
+
+
 def nova_lib(model):
     import nova_amd
     return nova_amd.load(model)

@@ -11,6 +11,10 @@ compiled unchanged -- and stores inputs and outputs only:
                       the full state (free list, refcounts, tables, n_past,
                       cow_count) after each op
   registry.json       BlockRegistry put/find sequences
+  q4k.npz             Q4_K blocks -> dequantised floats through the reference's
+                      own dequant_block (include/nova/quant/q4_k.h): the
+                      known-answer block of tests/selftest_q4k.cpp:31-38 and
+                      seeded random blocks (incl. subnormal / zero scales)
   attn_<model>.npz    decode (n_past = 9) and prefill (n_q = 3, n_past = 5)
                       outputs for the inputs of tests/sycl_bench.cpp:889-985
                       (xorshift Rng seed 0x9E3779B97F4A7C15, Q in [-1,1),
@@ -218,6 +222,27 @@ def attn_fixture(ref: Reference, model: str):
                 q_prefill=qp, prefill_n_q=np.int32(3), prefill_n_past=np.int32(5), prefill_out=pre)
 
 
+def q4k_fixture(ref: Reference):
+    import ctypes as C
+    L = ref.q4k
+    st = np.zeros(144, np.uint8)
+    L.ref_q4k_selftest_block(st.ctypes.data)
+    rng = np.random.default_rng(144)
+    blocks = rng.integers(0, 256, (24, 144), dtype=np.uint8)
+    ds = rng.uniform(1e-4, 2e-2, (24, 2)).astype(np.float16)
+    ds[3] = [np.float16(3e-6), np.float16(0)]       # subnormal scale, zero min scale
+    ds[4] = [np.float16(0), np.float16(1e-3)]
+    blocks[:, 0:4] = ds.view(np.uint8).reshape(24, 4)
+    blocks = np.concatenate([st[None], blocks])
+    y = np.empty((len(blocks), 256), np.float32)
+    for i, b in enumerate(blocks):
+        bb = np.ascontiguousarray(b)
+        L.ref_q4k_dequant_block(bb.ctypes.data, y[i].ctypes.data)
+    halves = np.array([0x0000, 0x0001, 0x03FF, 0x0400, 0x3C00, 0xBC00, 0x7BFF, 0x2C00, 0x1A00], np.uint16)
+    hv = np.array([L.ref_q4k_half(C.c_uint16(int(h))) for h in halves], np.float32)
+    return dict(blocks=blocks, y=y, halves=halves, half_values=hv)
+
+
 def main():
     ref = Reference()
     (HERE / "kv_hash.json").write_text(json.dumps(hash_fixture(ref), indent=1))
@@ -229,6 +254,7 @@ def main():
     (HERE / "registry.json").write_text(json.dumps(registry_fixture(ref)))
     for model in ("qwen25_7b", "qwen25_1p5b"):
         np.savez_compressed(HERE / f"attn_{model}.npz", **attn_fixture(ref, model))
+    np.savez_compressed(HERE / "q4k.npz", **q4k_fixture(ref))
     for p in sorted(HERE.iterdir()):
         print(p.name, p.stat().st_size)
 

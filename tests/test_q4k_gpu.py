@@ -1,0 +1,70 @@
+"""Parity of the gfx950 Q4_K GEMV and activation quantiser against the CPU
+oracle (or_quant_q8 restating quant_kernel, src/kernel/q4k_gemv.cu:9-33;
+or_gemv_q4k: the dequantised product in double, the value gemv_kernel
+q4k_gemv.cu:35-91 computes in fp32).
+
+Quantisation is bit-exact (IEEE divide and round-to-nearest-even on both
+sides).  The GEMV sums in fp32 in its own order: the tolerance is 2e-6 of the
+row's sum of |terms| (the reference's own self-test allows 1e-5 of one block,
+tests/selftest_q4k.cpp:72-74)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def random_blocks(rng, rows, cols):
+    b = rng.integers(0, 256, (rows, cols // 256, 144), dtype=np.uint8)
+    b[..., 0:2] = rng.uniform(2e-4, 4e-3, (rows, cols // 256, 1)).astype(np.float16).view(np.uint8)
+    b[..., 2:4] = rng.uniform(1e-4, 2e-3, (rows, cols // 256, 1)).astype(np.float16).view(np.uint8)
+    return b
+
+
+def abs_terms(oracle, w, rows, cols, qs, d):
+    """sum over k of |w_rk * x_k| (dequantised), for the tolerance"""
+    out = np.empty(rows)
+    xq = np.abs(qs[0].astype(np.float64) * np.repeat(d[0].astype(np.float64), 32))
+    for r in range(rows):
+        y = np.concatenate([oracle.q4k_dequant_block(w[r, b]) for b in range(cols // 256)]).astype(np.float64)
+        out[r] = np.abs(y) @ xq
+    return out
+
+
+@pytest.mark.parametrize("rows,cols", [(3, 3584), (1, 18944), (2, 256), (4, 32768)])
+def test_quant_bit_exact(rows, cols, nova7, oracle):
+    nova = nova7
+    print(f"[case] quant rows={rows} cols={cols}", flush=True)
+    rng = np.random.default_rng(cols + rows)
+    x = (rng.standard_normal((rows, cols)) * rng.uniform(0.01, 20, (rows, 1))).astype(np.float32)
+    x[0, 64:96] = 0.0                                          # an all-zero block
+    dx = nova.upload(x)
+    qs, d, s = nova.alloc(rows * cols), nova.alloc(rows * cols // 8), nova.alloc(rows * cols // 4)
+    nova.launch_quant_q8(qs.ptr, d.ptr, s.ptr, dx.ptr, rows, cols, None)
+    nova.dev_sync()
+    rq, rd, rs = oracle.quant_q8(x)
+    assert np.array_equal(qs.numpy((rows, cols), np.int8), rq)
+    assert np.array_equal(d.numpy((rows, cols // 32), np.float32), rd)
+    assert np.array_equal(s.numpy((rows, cols // 16), np.int32), rs)
+
+
+@pytest.mark.parametrize("rows,cols", [(37, 256), (512, 3584), (3584, 3584), (130, 18944), (9, 32768),
+                                       (1000, 2560)])
+def test_gemv_matches_oracle(rows, cols, nova7, oracle):
+    nova = nova7
+    print(f"[case] gemv rows={rows} cols={cols}", flush=True)
+    rng = np.random.default_rng(rows * 7 + cols)
+    w = random_blocks(rng, rows, cols)
+    x = rng.standard_normal((1, cols)).astype(np.float32)
+    qs, d, s = oracle.quant_q8(x)
+    dw, dq, dd, ds = nova.upload(w), nova.upload(qs), nova.upload(d), nova.upload(s)
+    out = nova.upload(np.full(rows, np.nan, np.float32))
+    nova.launch_gemv_q4k(dw.ptr, rows, cols, dq.ptr, dd.ptr, ds.ptr, out.ptr, None)
+    nova.dev_sync()
+    got = out.numpy((rows,), np.float32).astype(np.float64)
+    ref = oracle.gemv_q4k(w, rows, cols, qs, d, s)
+    check = slice(None) if rows <= 600 else slice(0, rows, max(rows // 300, 1))
+    scale = abs_terms(oracle, w[check], len(range(rows)[check]), cols, qs, d)
+    err = np.abs(got[check] - ref[check])
+    assert np.all(np.isfinite(got))
+    assert np.all(err <= 2e-6 * scale), f"max err/scale {np.max(err / scale):.2e}"
+    print(f"  max |gpu-oracle| / sum|terms| = {np.max(err / scale):.2e}")

@@ -16,9 +16,11 @@
 //  * A wave covers 8 super-blocks per step: lane (j, c) = (lane >> 3, lane & 7)
 //    takes the 16 nibble bytes at offset 16c of super-block 8s + j -- 16 weights
 //    of sub-block 2(c>>1) (low nibbles) and 16 of sub-block 2(c>>1)+1 (high).
-//    Loads go out 4 steps (32 super-blocks, 4.6 KiB per wave) at a time
-//    before any is consumed; at ~70 registers many waves share a CU, which
-//    keeps enough bytes in flight.
+//    Rows of up to 4 steps (cols <= 8192: the hidden widths 1536, 3584,
+//    5120) use a kernel whose step loop is unrolled at compile time, all of a
+//    row's loads issued before any is consumed; wider rows (the FFN widths)
+//    take 4 steps in flight at a time.  One row per wave either way; ~70-80
+//    registers keep 6-7 waves per SIMD resident.
 //  * Products: v_dot4_i32_i8 on nibbles unpacked with a mask and a shift
 //    (8 per lane per super-block); the per-sub-block float combination is the
 //    reference's; the row sum is a wave reduction.
@@ -96,6 +98,87 @@ __device__ __forceinline__ void scale_min(int j, const uint32_t sw[3], uint32_t&
     }
 }
 
+// one lane's share of super-block sb (header hd, nibbles nb16) against the
+// activation staged in LDS: the two sub-block terms of the reference's sum
+__device__ __forceinline__ float sb_terms(const u4 hd, const u4 nb16, int sb, int grp, int elo,
+                                          const int8_t* s_q, const float* s_d, const int32_t* s_s) {
+    const int k0 = sb * kQK + elo;             // low-nibble elements k0..k0+15, high k0+32..
+    const i4 alo = *reinterpret_cast<const i4*>(s_q + k0);
+    const i4 ahi = *reinterpret_cast<const i4*>(s_q + k0 + 32);
+    int dlo = 0, dhi = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        dlo = __builtin_amdgcn_sdot4((int)(nb16[e] & 0x0F0F0F0Fu), alo[e], dlo, false);
+        dhi = __builtin_amdgcn_sdot4((int)((nb16[e] >> 4) & 0x0F0F0F0Fu), ahi[e], dhi, false);
+    }
+    const uint32_t sw[3] = {hd[1], hd[2], hd[3]};
+    uint32_t scl, mcl, sch, mch;
+    scale_min(2 * grp, sw, scl, mcl);
+    scale_min(2 * grp + 1, sw, sch, mch);
+    const float dd = half_to_float(hd[0] & 0xFFFFu);
+    const float dm = half_to_float(hd[0] >> 16);
+    const float dxl = s_d[k0 >> 5], dxh = s_d[(k0 + 32) >> 5];
+    const int sml = s_s[k0 >> 4], smh = s_s[(k0 + 32) >> 4];
+    return dxl * ((dd * (float)scl) * (float)dlo - (dm * (float)mcl) * (float)sml) +
+           dxh * ((dd * (float)sch) * (float)dhi - (dm * (float)mch) * (float)smh);
+}
+
+__device__ __forceinline__ void stage_activation(int cols, const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                 const int32_t* __restrict__ xs, int8_t* s_q, float* s_d,
+                                                 int32_t* s_s) {
+    for (int i = threadIdx.x; i < cols / 16; i += QT)
+        *reinterpret_cast<u4*>(s_q + 16 * i) = *reinterpret_cast<const u4*>(xq + 16 * i);
+    for (int i = threadIdx.x; i < cols / 32; i += QT) s_d[i] = xd[i];
+    for (int i = threadIdx.x; i < cols / 16; i += QT) s_s[i] = xs[i];
+    __syncthreads();
+}
+
+// Rows of at most 4 steps (8 super-blocks per step, cols <= 8192): the step
+// loop is unrolled at compile time, one row per wave, all of the row's loads
+// issued before any is consumed.  (Measured on gfx950: taking 2 or 4 rows per
+// wave at once keeps more bytes in flight per wave but costs occupancy and is
+// slower; so is a compile-time kernel for the 10-step rows of the FFN width.)
+template <int STEPS>
+__global__ void __launch_bounds__(QT) gemv_fixed_kernel(const uint8_t* __restrict__ w, int64_t rows, int cols,
+                                                         const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                         const int32_t* __restrict__ xs, float* __restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char s_x[];
+    int8_t* s_q = reinterpret_cast<int8_t*>(s_x);
+    float* s_d = reinterpret_cast<float*>(s_x + cols);
+    int32_t* s_s = reinterpret_cast<int32_t*>(s_x + cols + 4 * (cols / 32));
+    stage_activation(cols, xq, xd, xs, s_q, s_d, s_s);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int j = lane >> 3, c = lane & 7, grp = c >> 1;
+    const int elo = grp * 64 + (c & 1) * 16;
+    const int nsb = cols / kQK;
+    const int64_t row_bytes = (int64_t)nsb * kBlockBytes;
+
+    for (int64_t r = (int64_t)blockIdx.x * 4 + wave; r < rows; r += (int64_t)gridDim.x * 4) {
+        u4 hdr[STEPS], nib[STEPS];
+#pragma unroll
+        for (int t = 0; t < STEPS; ++t) {
+            const int sb = 8 * t + j;
+            if (sb < nsb) {
+                const uint8_t* blk = w + r * row_bytes + (int64_t)sb * kBlockBytes;
+                hdr[t] = *reinterpret_cast<const u4*>(blk);
+                nib[t] = *reinterpret_cast<const u4*>(blk + 16 + 16 * c);
+            }
+        }
+        float acc = 0.f;
+#pragma unroll
+        for (int t = 0; t < STEPS; ++t) {
+            const int sb = 8 * t + j;
+            if (sb < nsb) acc += sb_terms(hdr[t], nib[t], sb, grp, elo, s_q, s_d, s_s);
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        if (lane == 0) out[r] = acc;
+    }
+}
+
+// Any width: one row per wave, 4 steps of loads in flight at a time.
 __global__ void __launch_bounds__(QT) gemv_kernel(const uint8_t* __restrict__ w, int64_t rows, int cols,
                                                    const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                    const int32_t* __restrict__ xs, float* __restrict__ out) {
@@ -103,11 +186,7 @@ __global__ void __launch_bounds__(QT) gemv_kernel(const uint8_t* __restrict__ w,
     int8_t* s_q = reinterpret_cast<int8_t*>(s_x);
     float* s_d = reinterpret_cast<float*>(s_x + cols);
     int32_t* s_s = reinterpret_cast<int32_t*>(s_x + cols + 4 * (cols / 32));
-    for (int i = threadIdx.x; i < cols / 16; i += QT)
-        *reinterpret_cast<u4*>(s_q + 16 * i) = *reinterpret_cast<const u4*>(xq + 16 * i);
-    for (int i = threadIdx.x; i < cols / 32; i += QT) s_d[i] = xd[i];
-    for (int i = threadIdx.x; i < cols / 16; i += QT) s_s[i] = xs[i];
-    __syncthreads();
+    stage_activation(cols, xq, xd, xs, s_q, s_d, s_s);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -136,27 +215,7 @@ __global__ void __launch_bounds__(QT) gemv_kernel(const uint8_t* __restrict__ w,
 #pragma unroll
             for (int t = 0; t < kBatch; ++t) {
                 const int sb = 8 * (t0 + t) + j;
-                if (sb < nsb) {
-                    const int k0 = sb * kQK + elo;         // low-nibble elements k0..k0+15, high k0+32..
-                    const i4 alo = *reinterpret_cast<const i4*>(s_q + k0);
-                    const i4 ahi = *reinterpret_cast<const i4*>(s_q + k0 + 32);
-                    int dlo = 0, dhi = 0;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        dlo = __builtin_amdgcn_sdot4((int)(nib[t][e] & 0x0F0F0F0Fu), alo[e], dlo, false);
-                        dhi = __builtin_amdgcn_sdot4((int)((nib[t][e] >> 4) & 0x0F0F0F0Fu), ahi[e], dhi, false);
-                    }
-                    const uint32_t sw[3] = {hdr[t][1], hdr[t][2], hdr[t][3]};
-                    uint32_t scl, mcl, sch, mch;
-                    scale_min(2 * grp, sw, scl, mcl);
-                    scale_min(2 * grp + 1, sw, sch, mch);
-                    const float dd = half_to_float(hdr[t][0] & 0xFFFFu);
-                    const float dm = half_to_float(hdr[t][0] >> 16);
-                    const float dxl = s_d[k0 >> 5], dxh = s_d[(k0 + 32) >> 5];
-                    const int sml = s_s[k0 >> 4], smh = s_s[(k0 + 32) >> 4];
-                    acc += dxl * ((dd * (float)scl) * (float)dlo - (dm * (float)mcl) * (float)sml);
-                    acc += dxh * ((dd * (float)sch) * (float)dhi - (dm * (float)mch) * (float)smh);
-                }
+                if (sb < nsb) acc += sb_terms(hdr[t], nib[t], sb, grp, elo, s_q, s_d, s_s);
             }
         }
 #pragma unroll
@@ -175,6 +234,13 @@ int gemv_grid(int64_t rows) {
     const int64_t want = (rows + 3) / 4;       // one row per wave
     const int64_t cap = (int64_t)cus * 8;      // grid-stride beyond 8 workgroups per CU
     return (int)(want < cap ? want : cap);
+}
+
+template <int STEPS>
+void launch_fixed(const uint8_t* blocks, int64_t rows, int cols, const int8_t* xq, const float* xd,
+                  const int32_t* xs, float* out, size_t lds, hipStream_t s) {
+    hipLaunchKernelGGL(gemv_fixed_kernel<STEPS>, dim3((unsigned)gemv_grid(rows)), dim3(QT), lds, s, blocks, rows,
+                       cols, xq, xd, xs, out);
 }
 
 }  // namespace
@@ -199,8 +265,16 @@ void launch_gemv_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_t
     NOVA_REQUIRE(cols > 0 && cols % kQK == 0 && cols <= kMaxCols);
     if (rows == 0) return;
     const size_t lds = (size_t)cols + 4 * (size_t)(cols / 32) + 4 * (size_t)(cols / 16);
-    hipLaunchKernelGGL(gemv_kernel, dim3((unsigned)gemv_grid(rows)), dim3(QT), lds, reinterpret_cast<hipStream_t>(s),
-                       blocks, rows, cols, xq, xd, xs, out);
+    const hipStream_t st = reinterpret_cast<hipStream_t>(s);
+    switch ((cols / kQK + 7) / 8) {            // steps of 8 super-blocks
+        case 1: launch_fixed<1>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
+        case 2: launch_fixed<2>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
+        case 3: launch_fixed<3>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
+        case 4: launch_fixed<4>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
+        default:
+            hipLaunchKernelGGL(gemv_kernel, dim3((unsigned)gemv_grid(rows)), dim3(QT), lds, st, blocks, rows, cols,
+                               xq, xd, xs, out);
+    }
     NOVA_LAUNCHED();
 }
 

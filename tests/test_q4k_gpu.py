@@ -47,8 +47,9 @@ def test_quant_bit_exact(rows, cols, nova7, oracle):
     assert np.array_equal(s.numpy((rows, cols // 16), np.int32), rs)
 
 
-@pytest.mark.parametrize("rows,cols", [(37, 256), (512, 3584), (3584, 3584), (130, 18944), (9, 32768),
-                                       (1000, 2560)])
+@pytest.mark.parametrize("rows,cols", [(37, 256), (20, 1536), (512, 3584), (3584, 3584), (50, 5120), (11, 8192),
+                                       (70, 8960), (33, 13824), (130, 18944), (9, 32768), (1000, 2560),
+                                       (1, 3584), (3, 18944)])
 def test_gemv_matches_oracle(rows, cols, nova7, oracle):
     nova = nova7
     print(f"[case] gemv rows={rows} cols={cols}", flush=True)

@@ -72,6 +72,11 @@ def _abort_run(code):
     ("n.launch_attn_decode_paged(1, 1, 1, 1, 99, 4, 5, 1, 1, None)", "layer < Model::L"),
     ("n.launch_kv_store_paged(1, 1, 1, 0, 0, 1, 0, 1, 1, None)", "nb > 0"),
     ("n.launch_attn_prefill_paged(0, 1, 1, 1, 0, 4, 1, 0, 1, None)", "q && pool_k"),
+    ("n.launch_gemv_q4k(1, 4, 300, 1, 1, 1, 1, None)", "cols % kQK == 0"),
+    ("n.launch_gemv_q4k(1, 4, 65536, 1, 1, 1, 1, None)", "cols <= kMaxCols"),
+    ("n.launch_quant_q8(1, 1, 1, 1, 1, 33, None)", "cols % 32 == 0"),
+    ("n.launch_rope_kv_store_paged(1, 1, 1, 1, 1, 1, 1, 1, 28, 4, 1, 0, None)", "layer < Model::L"),
+    ("n.launch_rope_batch(1, 1, 2, -1, 1, 1, None)", "pos0 >= 0"),
 ])
 def test_bad_arguments_abort_before_launch(call, needle):
     """the reference's abort-only convention (include/nova/config.h:42-63):

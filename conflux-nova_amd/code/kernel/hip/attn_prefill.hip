@@ -13,7 +13,13 @@
 //    of one (session, kv head); two workgroups share a CU (2 waves per SIMD, so
 //    one wave's softmax overlaps the other's MFMAs).  NB = 2 when the launch
 //    has enough (session, column group) items to fill the chip, NB = 1 (twice
-//    the workgroups) for small launches such as one session's chunk.
+//    the workgroups) for small launches such as one session's chunk.  Those
+    small launches also split the keys: their workgroups hold two groups of 4
+    waves over the same columns, group g taking key tiles g, g+2, ..., each
+    with its own LDS ring, and the two partial (O, l, m) are merged through
+    LDS at the end (measured: one session's chunk 16% faster; with NB = 2
+    the second group spills registers and is 26% slower, so wide launches
+    keep one group).
 //  * K/V tiles of 32 keys (2 pages) are staged ONCE per workgroup in LDS by
 //    direct global->LDS loads (global_load_lds_dwordx4: no staging
 //    registers), four buffers: while tile t's softmax runs, the scores of
@@ -131,24 +137,25 @@ __device__ __forceinline__ int item_bucket(const PrefillArgs& a, int j, int n_cg
 
 // The item of rank r in decreasing cost order (ties in index order).  Every
 // thread of the workgroup calls it (it has barriers) and gets the same answer.
-// s_i: LDS scratch of kBuckets + THREADS + 16 ints.
+// s_i: LDS scratch of kBuckets + NT + 16 ints; NT threads in the workgroup.
+template <int NT>
 __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int cols_wg, int* s_i) {
     const int N = a.n_sess * n_cg;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int* hist = s_i;
     int* part = s_i + kBuckets;
-    int* res = part + THREADS;          // [0] group, [1] ranks above it, [2] item, [4..] wave counts
-    for (int b = tid; b < kBuckets; b += THREADS) hist[b] = 0;
+    int* res = part + NT;          // [0] group, [1] ranks above it, [2] item, [4..] wave counts
+    for (int b = tid; b < kBuckets; b += NT) hist[b] = 0;
     __syncthreads();
-    for (int j = tid; j < N; j += THREADS) atomicAdd(&hist[item_bucket(a, j, n_cg, n_cols, cols_wg)], 1);
+    for (int j = tid; j < N; j += NT) atomicAdd(&hist[item_bucket(a, j, n_cg, n_cols, cols_wg)], 1);
     __syncthreads();
-    constexpr int PER = kBuckets / THREADS;
+    constexpr int PER = kBuckets / NT;
     int sum = 0;
 #pragma unroll
     for (int u = 0; u < PER; ++u) sum += hist[PER * tid + u];
     part[tid] = sum;
     __syncthreads();
-    constexpr int GPL = THREADS / 64;   // groups per lane
+    constexpr int GPL = NT / 64;   // groups per lane
     if (wave == 0) {
         // lane l covers groups GPL*l .. GPL*l+GPL-1; ranks run from the highest group down
         int ls = 0;
@@ -183,7 +190,7 @@ __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int c
         base += h;
     }
     // the o-th item (index order) whose cost falls in that bucket
-    for (int j0 = 0; j0 < N; j0 += THREADS) {
+    for (int j0 = 0; j0 < N; j0 += NT) {
         const int j = j0 + tid;
         const bool f = j < N && item_bucket(a, j, n_cg, n_cols, cols_wg) == bucket;
         const uint64_t bal = __builtin_amdgcn_ballot_w64(f);
@@ -191,7 +198,7 @@ __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int c
         __syncthreads();
         int before = 0, total = 0;
 #pragma unroll
-        for (int ww = 0; ww < WAVES; ++ww) {
+        for (int ww = 0; ww < NT / 64; ++ww) {
             const int n = res[4 + ww];
             before += ww < wave ? n : 0;
             total += n;
@@ -273,20 +280,28 @@ __device__ __forceinline__ uint32_t swz_v(int row, int chunk) {
     return (uint32_t)(row * ROWB + ((chunk ^ (2 * (row & 7))) << 4));
 }
 
-// two workgroups per CU (<= 256 registers per wave): while one wave runs its
-// softmax on the VALU the other wave of the SIMD keeps the matrix core busy
-template <int NB>                                // 16-column blocks per wave
-__global__ void __launch_bounds__(THREADS, 2)   // 2 waves per SIMD: <= 256 VGPRs
+// NB: 16-column blocks per wave.  KS: key groups -- KS groups of 4 waves
+// share the workgroup's columns; group k takes the key tiles KS*i + k with
+// its own ring of tile buffers, and the groups' softmax states are merged at
+// the end.  2 waves per SIMD either way (<= 256 VGPRs): two 4-wave
+// workgroups per CU (KS = 1) or one 8-wave workgroup (KS = 2); while one wave
+// runs its softmax on the VALU the other keeps the matrix core busy.
+template <int NB, int KS>
+__global__ void __launch_bounds__(THREADS * KS, 2)
 prefill_kernel(PrefillArgs a) {
+    constexpr int NT = THREADS * KS;
     constexpr int COLS_WAVE = 16 * NB;
     constexpr int COLS_WG = COLS_WAVE * WAVES;
-    __shared__ __attribute__((aligned(16))) unsigned char s_kv[NBUF][STAGE_BYTES];
+    __shared__ __attribute__((aligned(16))) unsigned char s_kv[KS][NBUF][STAGE_BYTES];
     __shared__ int32_t s_tab[kTabWin];
-    static_assert((kBuckets + THREADS + 16) * 4 <= (int)sizeof(s_kv), "ranking scratch fits the tile buffers");
-    static_assert(4 + WAVES <= 16 && kBuckets % THREADS == 0, "ranking scratch layout");
+    static_assert((kBuckets + NT + 16) * 4 <= (int)sizeof(s_kv), "ranking scratch fits the tile buffers");
+    static_assert(4 + NT / 64 <= 16 && kBuckets % NT == 0, "ranking scratch layout");
+    static_assert(KS == 1 || KS * 64 * NB * 34 * 4 * WAVES / KS <= (int)sizeof(s_kv), "merge scratch");
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    const int kg = tid / THREADS;                // key group
+    const int wave = (tid >> 6) & (WAVES - 1);   // wave within the group: its columns
+    const int gtid = tid & (THREADS - 1);
     const int lane = tid & 63;
     const int g = lane >> 4;
     const int c = lane & 15;
@@ -300,7 +315,7 @@ prefill_kernel(PrefillArgs a) {
     if (rank >= N) return;                                  // grid padding (uniform)
     int item;
     if (a.n_sess == 1 || N > kRankMax) item = (rank / n_cg) * n_cg + (n_cg - 1 - rank % n_cg);
-    else item = lpt_item(a, rank, n_cg, n_cols, COLS_WG, reinterpret_cast<int*>(&s_kv[0][0]));
+    else item = lpt_item<NT>(a, rank, n_cg, n_cols, COLS_WG, reinterpret_cast<int*>(&s_kv[0][0][0]));
     const int sess = item / n_cg;
     const int cg = item - sess * n_cg;
     const int n_past = n_past_of(a, sess);
@@ -312,6 +327,7 @@ prefill_kernel(PrefillArgs a) {
     const int wg_col_last = min(wg_col0 + COLS_WG, n_cols) - 1;
     const int key_end = n_past + wg_col_last / G + 1;         // keys the workgroup needs
     const int n_tiles = (key_end + TILE - 1) / TILE;
+    const int n_steps = (n_tiles + KS - 1) / KS;               // tiles per key group (rounded up)
     const int col0 = wg_col0 + wave * COLS_WAVE;
     const int wave_last = min(col0 + COLS_WAVE, n_cols) - 1;
     const int wave_key_end = col0 < n_cols ? n_past + wave_last / G + 1 : 0;
@@ -328,29 +344,33 @@ prefill_kernel(PrefillArgs a) {
     const char* pv = reinterpret_cast<const char*>(a.pool_v);
     const int64_t layer_page0 = (int64_t)a.layer * a.nb;
     const int n_pages = (key_end + kKvBlock - 1) >> kKvBlockShift;
-    const int srow = tid >> 4;                               // row inside the page
-    const int schunk_k = (tid & 15) ^ srow;                  // global chunk this lane moves (K, V)
-    const int schunk_v = (tid & 15) ^ (2 * (srow & 7));
+    const int srow = gtid >> 4;                              // row inside the page
+    const int schunk_k = (gtid & 15) ^ srow;                 // global chunk this lane moves (K, V)
+    const int schunk_v = (gtid & 15) ^ (2 * (srow & 7));
     const uint32_t loff_k = (uint32_t)(srow * (KVW * 2) + 16 * schunk_k);
     const uint32_t loff_v = (uint32_t)(srow * (KVW * 2) + 16 * schunk_v);
     const uint32_t wave_s = __builtin_amdgcn_readfirstlane(wave);
     int win0 = 0;                                            // first page of the LDS table window
     auto load_window = [&](int first) {                      // every thread, uniform
-        for (int e = tid; e < kTabWin && first + e < n_pages; e += THREADS) s_tab[e] = table[first + e];
+        for (int e = tid; e < kTabWin && first + e < n_pages; e += NT) s_tab[e] = table[first + e];
         __syncthreads();
         win0 = first;
     };
     load_window(0);
-    // physical pages of tile T, read from the LDS table a step before the
-    // loads that use them (the window only moves forward, between barriers,
-    // with every wave calling this at the same point)
+    // physical pages of this group's tile of step i (tile KS*i + kg), read
+    // from the LDS table a step before the loads that use them.  Every wave
+    // calls this at the same points with the same i, so the window (which
+    // only moves forward, between barriers) is moved by all of them together.
     struct Pages { int p0, p1; };
-    auto read_pages = [&](int T) -> Pages {
-        const int pg0 = 2 * T;
-        if (pg0 - win0 >= kTabWin) {
+    auto read_pages = [&](int i) -> Pages {
+        const int pg_first = 2 * KS * i;                     // first page of step i's tiles
+        if (pg_first < n_pages && pg_first + 2 * KS - 1 - win0 >= kTabWin) {
             __syncthreads();                                 // every wave is done with the old window
-            load_window(pg0);
+            load_window(pg_first);
         }
+        const int T = KS * i + kg;
+        if (T >= n_tiles) return Pages{0, 0};                // no such tile for this group
+        const int pg0 = 2 * T;
         const int pg1 = pg0 + 1 < n_pages ? pg0 + 1 : pg0;   // a lone last page loads itself twice
         return Pages{s_tab[pg0 - win0], s_tab[pg1 - win0]};
     };
@@ -358,7 +378,7 @@ prefill_kernel(PrefillArgs a) {
         constexpr int BI = decltype(buf_tag)::value;
         const int64_t b0 = (layer_page0 + __builtin_amdgcn_readfirstlane(pp.p0)) * kPageBytes + kvh * ROWB;
         const int64_t b1 = (layer_page0 + __builtin_amdgcn_readfirstlane(pp.p1)) * kPageBytes + kvh * ROWB;
-        const uint32_t m0base = lds_addr(&s_kv[BI][0]) + 1024u * wave_s;
+        const uint32_t m0base = __builtin_amdgcn_readfirstlane(lds_addr(&s_kv[kg][BI][0])) + 1024u * wave_s;
         if (TILE * (T + 1) <= key_end) {
 #pragma unroll
             for (int u = 0; u < LOADS; ++u)
@@ -380,11 +400,14 @@ prefill_kernel(PrefillArgs a) {
         }
     };
 
-    Pages pp{0, 0};
-    if (n_tiles > 0) load_tile(std::integral_constant<int, 0>{}, 0, read_pages(0));
-    if (n_tiles > 1) load_tile(std::integral_constant<int, 1>{}, 1, read_pages(1));
-    if (n_tiles > 2) load_tile(std::integral_constant<int, 2>{}, 2, read_pages(2));
-    if (n_tiles > 3) pp = read_pages(3);
+    // the group's tiles of steps 0, 1, 2 start loading; step 3's pages are read
+    Pages pp = read_pages(0);
+    if (kg < n_tiles) load_tile(std::integral_constant<int, 0>{}, kg, pp);
+    pp = read_pages(1);
+    if (KS + kg < n_tiles) load_tile(std::integral_constant<int, 1>{}, KS + kg, pp);
+    pp = read_pages(2);
+    if (2 * KS + kg < n_tiles) load_tile(std::integral_constant<int, 2>{}, 2 * KS + kg, pp);
+    pp = read_pages(3);
 
     // ---- Q^T operands: lane (g,c) of block b holds column col0 + 16b + c ----
     h8 qh[NB][4];
@@ -432,24 +455,27 @@ prefill_kernel(PrefillArgs a) {
     // K rows c (page 0) and 16 + c (page 1), chunk 4ks + g; V^T: lane s of
     // group g reads key row 4g + (s >> 2) (and +16, the second page), halfs
     // 16cb + 4 (s & 3) .. +3 of it
+    // (the group's ring is folded into the lane offsets)
     uint32_t koff[4], voff[8];
+    const uint32_t ring = (uint32_t)kg * NBUF * STAGE_BYTES;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) koff[ks] = swz_k(c, 4 * ks + g);
+    for (int ks = 0; ks < 4; ++ks) koff[ks] = ring + swz_k(c, 4 * ks + g);
     {
         const int vr = 4 * g + (c >> 2);
         const int vh = (c >> 1) & 1;
 #pragma unroll
-        for (int cb = 0; cb < 8; ++cb) voff[cb] = TILE * ROWB + swz_v(vr, 2 * cb + vh) + 8 * (c & 1);
+        for (int cb = 0; cb < 8; ++cb) voff[cb] = ring + TILE * ROWB + swz_v(vr, 2 * cb + vh) + 8 * (c & 1);
     }
+    const unsigned char* s_ring0 = &s_kv[0][0][0];
 
-    // tiles 0 and 1 resident (tile 2 may still be loading)
-    if (n_tiles > 2) tile_barrier<LOADS>();
+    // the group's tiles of steps 0 and 1 resident (step 2's may still be loading)
+    if (2 * KS + kg < n_tiles) tile_barrier<LOADS>();
     else tile_barrier<0>();
 
     // S^T = K . Q^T for both pages of the tile in buffer BI and all blocks
     auto compute_s = [&](auto buf_tag, f4 (&s0)[NB], f4 (&s1)[NB]) {
         constexpr int BI = decltype(buf_tag)::value;
-        const unsigned char* sk = s_kv[BI];
+        const unsigned char* sk = s_ring0 + BI * STAGE_BYTES;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const h8 k0 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + koff[ks]));
@@ -466,11 +492,11 @@ prefill_kernel(PrefillArgs a) {
     // basic block as this tile's row maxima so that the matrix core and the
     // VALU work side by side.  kMask selects the causal masking (only tiles
     // that cross the diagonal or the end of the keys need it).
-    auto tile = [&](auto mask_tag, auto buf_tag, auto next_tag, int key_base, const f4 (&c0)[NB],
+    auto tile = [&](auto mask_tag, auto buf_tag, auto next_tag, int key_base, bool first, const f4 (&c0)[NB],
                     const f4 (&c1)[NB], f4 (&n0)[NB], f4 (&n1)[NB]) {
         constexpr bool kMask = decltype(mask_tag)::value;
         constexpr int BI = decltype(buf_tag)::value;
-        const unsigned char* sv = s_kv[BI];
+        const unsigned char* sv = s_ring0 + BI * STAGE_BYTES;
         // V^T operands: va[cb] row c = d 16cb + c, k = keys kappa(g, j) =
         // (page j / 4, slot 4g + j % 4), the k order of P^T below
         h8 va[8];
@@ -519,16 +545,16 @@ prefill_kernel(PrefillArgs a) {
         bool over = false;
 #pragma unroll
         for (int b = 0; b < NB; ++b) over |= lmax[b] > kLazy;
-        if (__builtin_amdgcn_ballot_w64(over) || key_base == 0) {
-            // rare (and the first tile): move the max of every column whose
+        if (__builtin_amdgcn_ballot_w64(over) || first) {
+            // rare (and the group's first tile): move the max of every column whose
             // tile max exceeds it by more than kLazy.  bm = -inf: no key of the
             // column in this tile, nothing moves.
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 const float bm = rows_max(lmax[b]);
-                const bool need = bm > -INFINITY && (key_base == 0 || bm > kLazy);
+                const bool need = bm > -INFINITY && (first || bm > kLazy);
                 const float shift = need ? bm : 0.f;
-                const float corr = key_base == 0 ? 0.f : __builtin_amdgcn_exp2f(-shift);
+                const float corr = first ? 0.f : __builtin_amdgcn_exp2f(-shift);
                 lsum[b] *= corr;
 #pragma unroll
                 for (int cb = 0; cb < 8; ++cb) acc[b][cb] *= corr;
@@ -553,40 +579,68 @@ prefill_kernel(PrefillArgs a) {
         __builtin_amdgcn_s_setprio(0);
     };
 
-    // Tile pipeline over NBUF = 4 buffers.  Step t (buffer t % 4): issue the
-    // loads of tile t+3 into the buffer of tile t-1 and read tile t+4's pages;
-    // run tile t (its softmax and PV, with tile t+1's score MFMAs alongside);
-    // then the barrier makes tile t+2 resident (tile t+3 may stay in flight).
-    // A wave's last tile computes scores of a buffer it will not use: they are
-    // discarded.
-    const int wave_tiles = (wave_key_end + TILE - 1) / TILE;   // tiles this wave computes
+    // Tile pipeline over NBUF = 4 buffers per group.  Step i (buffer i % 4):
+    // issue the loads of the group's tile of step i+3 into the buffer of step
+    // i-1 and read step i+4's pages; run the group's tile of step i (softmax
+    // and PV, with step i+1's score MFMAs alongside); then the barrier makes
+    // step i+2's tile resident (step i+3's may stay in flight).  A wave's last
+    // tile computes scores of a buffer it will not use: they are discarded.
+    const int wave_tiles = (wave_key_end + TILE - 1) / TILE;   // tiles the wave's columns need
     f4 sa0[NB], sa1[NB], sb0[NB], sb1[NB];
-    if (wave_tiles > 0) compute_s(std::integral_constant<int, 0>{}, sa0, sa1);
-    auto step = [&](auto buf_tag, int t, f4 (&c0)[NB], f4 (&c1)[NB], f4 (&n0)[NB], f4 (&n1)[NB]) {
+    if (kg < wave_tiles) compute_s(std::integral_constant<int, 0>{}, sa0, sa1);
+    auto step = [&](auto buf_tag, int i, f4 (&c0)[NB], f4 (&c1)[NB], f4 (&n0)[NB], f4 (&n1)[NB]) {
         constexpr int BI = decltype(buf_tag)::value;
-        const bool ahead = t + 3 < n_tiles;
-        if (ahead) {
-            load_tile(std::integral_constant<int, (BI + 3) % NBUF>{}, t + 3, pp);
-            if (t + 4 < n_tiles) pp = read_pages(t + 4);
-        }
+        const int t = KS * i + kg;                           // the group's tile
+        const bool ahead = t + 3 * KS < n_tiles;
+        if (ahead) load_tile(std::integral_constant<int, (BI + 3) % NBUF>{}, t + 3 * KS, pp);
+        if (i + 4 < n_steps) pp = read_pages(i + 4);         // every wave, same i
         if (t < wave_tiles) {
             const int key_base = t * TILE;
             constexpr auto next = std::integral_constant<int, (BI + 1) % NBUF>{};
             // a tile needs no mask when every key in it exists and is visible
             // to every column of the wave
             if (key_base + TILE <= key_min_full)
-                tile(std::integral_constant<bool, false>{}, buf_tag, next, key_base, c0, c1, n0, n1);
+                tile(std::integral_constant<bool, false>{}, buf_tag, next, key_base, i == 0, c0, c1, n0, n1);
             else
-                tile(std::integral_constant<bool, true>{}, buf_tag, next, key_base, c0, c1, n0, n1);
+                tile(std::integral_constant<bool, true>{}, buf_tag, next, key_base, i == 0, c0, c1, n0, n1);
         }
         if (ahead) tile_barrier<LOADS>();
         else tile_barrier<0>();
     };
-    for (int t = 0; t < n_tiles; t += NBUF) {               // unrolled: buffers and score registers rotate
-        step(std::integral_constant<int, 0>{}, t, sa0, sa1, sb0, sb1);
-        if (t + 1 < n_tiles) step(std::integral_constant<int, 1>{}, t + 1, sb0, sb1, sa0, sa1);
-        if (t + 2 < n_tiles) step(std::integral_constant<int, 2>{}, t + 2, sa0, sa1, sb0, sb1);
-        if (t + 3 < n_tiles) step(std::integral_constant<int, 3>{}, t + 3, sb0, sb1, sa0, sa1);
+    for (int i = 0; i < n_steps; i += NBUF) {               // unrolled: buffers and score registers rotate
+        step(std::integral_constant<int, 0>{}, i, sa0, sa1, sb0, sb1);
+        if (i + 1 < n_steps) step(std::integral_constant<int, 1>{}, i + 1, sb0, sb1, sa0, sa1);
+        if (i + 2 < n_steps) step(std::integral_constant<int, 2>{}, i + 2, sa0, sa1, sb0, sb1);
+        if (i + 3 < n_steps) step(std::integral_constant<int, 3>{}, i + 3, sb0, sb1, sa0, sa1);
+    }
+
+    if constexpr (KS == 2) {
+        // merge group 1's (m, l, acc) into group 0's through LDS (the tile
+        // buffers are free: the last step ended with a barrier)
+        float* xs = reinterpret_cast<float*>(&s_kv[0][0][0]) + (wave * 64 + lane) * (NB * 34);
+        if (kg == 1) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb) *reinterpret_cast<f4*>(xs + b * 34 + 4 * cb) = acc[b][cb];
+                xs[b * 34 + 32] = lsum[b][0];
+                xs[b * 34 + 33] = m[b];
+            }
+        }
+        __syncthreads();
+        if (kg == 1) return;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float l1 = xs[b * 34 + 32], m1 = xs[b * 34 + 33], l0 = lsum[b][0];
+            // a group without keys for this column has l = 0 and must not set the max
+            const float mm = l1 > 0.f ? (l0 > 0.f ? fmaxf(m[b], m1) : m1) : m[b];
+            const float f0 = l0 > 0.f ? __builtin_amdgcn_exp2f(m[b] - mm) : 0.f;
+            const float f1 = l1 > 0.f ? __builtin_amdgcn_exp2f(m1 - mm) : 0.f;
+#pragma unroll
+            for (int cb = 0; cb < 8; ++cb)
+                acc[b][cb] = acc[b][cb] * f0 + *reinterpret_cast<const f4*>(xs + b * 34 + 4 * cb) * f1;
+            lsum[b] = f4{1.f, 1.f, 1.f, 1.f} * (l0 * f0 + l1 * f1);
+        }
     }
 
     // ---- normalise and store: lane (g,c) of block b holds d = 16cb + 4g + i ----
@@ -613,19 +667,32 @@ int compute_units() {
     return cus;
 }
 
+#ifndef NOVA_PREFILL_KS_WIDE
+#define NOVA_PREFILL_KS_WIDE 1
+#endif
+#ifndef NOVA_PREFILL_KS_NARROW
+#define NOVA_PREFILL_KS_NARROW 2
+#endif
+constexpr int kKsWide = NOVA_PREFILL_KS_WIDE;      // key groups with 128-column workgroups
+constexpr int kKsNarrow = NOVA_PREFILL_KS_NARROW;  // and with 64-column workgroups
+
 // Column groups of 128 (2 blocks per wave) when the launch has enough work
-// items to fill two workgroups per CU; otherwise of 64 (1 block per wave):
+// items to fill every workgroup slot of the chip (two 4-wave or one 8-wave
+// workgroup per CU); otherwise of 64 (1 block per wave):
 // twice the workgroups for a single session's chunk, each with half the
 // columns (same key tiles, half the work per tile).
 void launch(const PrefillArgs& a, int n_sess, hipStream_t s) {
+    const int64_t slots = (int64_t)compute_units() * (2 / kKsWide);
     const int64_t items128 = (a.n_q * G + 127) / 128 * (int64_t)n_sess * NKV;
-    const bool wide = items128 >= 2 * (int64_t)compute_units();
+    const bool wide = items128 >= slots;
     const int cols_wg = wide ? 128 : 64;
     const int64_t n_cg = (a.n_q * G + cols_wg - 1) / cols_wg;
     const int64_t n_wg = (n_cg * n_sess * NKV + kXcd - 1) / kXcd * kXcd;
     NOVA_REQUIRE(n_wg < (int64_t)1 << 31);
-    if (wide) hipLaunchKernelGGL(prefill_kernel<2>, dim3((unsigned)n_wg), dim3(THREADS), 0, s, a);
-    else hipLaunchKernelGGL(prefill_kernel<1>, dim3((unsigned)n_wg), dim3(THREADS), 0, s, a);
+    if (wide)
+        hipLaunchKernelGGL((prefill_kernel<2, kKsWide>), dim3((unsigned)n_wg), dim3(THREADS * kKsWide), 0, s, a);
+    else
+        hipLaunchKernelGGL((prefill_kernel<1, kKsNarrow>), dim3((unsigned)n_wg), dim3(THREADS * kKsNarrow), 0, s, a);
     NOVA_LAUNCHED();
 }
 

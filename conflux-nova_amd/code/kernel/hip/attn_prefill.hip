@@ -14,12 +14,12 @@
 //    one wave's softmax overlaps the other's MFMAs).  NB = 2 when the launch
 //    has enough (session, column group) items to fill the chip, NB = 1 (twice
 //    the workgroups) for small launches such as one session's chunk.  Those
-    small launches also split the keys: their workgroups hold two groups of 4
-    waves over the same columns, group g taking key tiles g, g+2, ..., each
-    with its own LDS ring, and the two partial (O, l, m) are merged through
-    LDS at the end (measured: one session's chunk 16% faster; with NB = 2
-    the second group spills registers and is 26% slower, so wide launches
-    keep one group).
+//    small launches also split the keys: their workgroups hold two groups of 4
+//    waves over the same columns, group g taking key tiles g, g+2, ..., each
+//    with its own LDS ring, and the two partial (O, l, m) are merged through
+//    LDS at the end (measured: one session's chunk 16% faster; with NB = 2
+//    the second group spills registers and is 26% slower, so wide launches
+//    keep one group).
 //  * K/V tiles of 32 keys (2 pages) are staged ONCE per workgroup in LDS by
 //    direct global->LDS loads (global_load_lds_dwordx4: no staging
 //    registers), four buffers: while tile t's softmax runs, the scores of

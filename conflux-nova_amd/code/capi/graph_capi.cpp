@@ -153,5 +153,16 @@ int nova_paged_cow_batch(nova_paged_t h, const int* sessions, const int64_t* pos
     return H(h)->cow_batch(ss.data(), pos0, n, count, st);
 }
 int32_t* nova_paged_table_dev(nova_paged_t h, int s) { return S(&H(h)->pool(), s).table_dev; }
+int nova_paged_create_sessions(nova_paged_t h, int count, int clear_pages, int* ids) {
+    if (count < 0 || (count > 0 && !ids)) {
+        std::fprintf(stderr, "[nova] FATAL: nova_paged_create_sessions: bad arguments\n");
+        std::abort();
+    }
+    return H(h)->create_sessions(count, clear_pages != 0, ids);
+}
+void nova_paged_push_tables(nova_paged_t h, const int* ids, int count) {
+    for (int i = 0; i < count; ++i) (void)S(&H(h)->pool(), ids[i]);   // validates every id
+    H(h)->push_tables(ids, count);
+}
 
 }  // extern "C"

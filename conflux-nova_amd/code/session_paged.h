@@ -17,12 +17,17 @@
 //     table patch rides in the same launch
 //   * cow_batch() applies the COW decisions of many sessions in one launch (the
 //     reference decides per session per block and copies each immediately)
+//   * create_sessions() / push_tables() serve many sessions at once: one table
+//     upload per run of consecutive slice ids (tables are rows of one device
+//     array) and one page-clear launch, where the reference uploads and clears
+//     per session
 // Errors abort, as in the reference: pool exhaustion during COW prints
 // "[FATAL] KV pool full during COW" (model.cpp:173), no free slice exits with 3
 // (session.h:88,99).
 #pragma once
 #include <cstdint>
 #include <cstdio>
+#include <algorithm>
 #include <cstdlib>
 #include <vector>
 
@@ -83,6 +88,62 @@ public:
     }
 
     void destroy_session(KvSlice* s) { pool_.release(s); }
+
+    // count sessions at once: acquire in order (the ids a serial caller would
+    // get), one upload per run of consecutive ids, one clear of all their
+    // pages.  Returns the number created; stops early (after the creations so
+    // far) with -1 in the remaining ids when the pool runs out of slices.
+    int create_sessions(int count, bool clear_pages, int* ids) {
+        std::vector<int> got;
+        got.reserve((size_t)count);
+        for (int j = 0; j < count; ++j) {
+            KvSlice* sl = pool_.acquire();
+            if (!sl) break;
+            sl->k = k_;
+            sl->v = v_;
+            got.push_back(sl->id);
+        }
+        for (int j = 0; j < count; ++j) ids[j] = j < (int)got.size() ? got[(size_t)j] : -1;
+        push_tables(got.data(), (int)got.size());
+        if (clear_pages && !got.empty()) {
+            std::vector<int32_t> pages;
+            for (int id : got) {
+                const KvSlice& sl = *pool_.slice(id);
+                pages.insert(pages.end(), sl.table.begin(), sl.table.end());
+            }
+            int32_t* d = static_cast<int32_t*>(dev_alloc(pages.size() * 4));
+            dev_upload_async(d, pages.data(), pages.size() * 4, stream_);
+            launch_kv_zero_pages(k_, v_, nb_, d, (int)pages.size(), stream_);
+            dev_stream_sync(stream_);
+            dev_free(d);
+        }
+        dev_stream_sync(stream_);
+        return (int)got.size();
+    }
+
+    // Upload the host tables of several sessions: ids are sorted and each run
+    // of consecutive ids goes up as one copy of adjacent device rows.
+    void push_tables(const int* ids, int count) {
+        if (count <= 0) return;
+        std::vector<int> v(ids, ids + count);
+        std::sort(v.begin(), v.end());
+        v.erase(std::unique(v.begin(), v.end()), v.end());
+        const size_t nbk = (size_t)pool_.nblocks();
+        size_t j = 0;
+        while (j < v.size()) {
+            size_t e = j + 1;
+            while (e < v.size() && v[e] == v[e - 1] + 1) ++e;
+            staging_.resize((e - j) * nbk);
+            for (size_t t = j; t < e; ++t) {
+                const KvSlice& sl = *pool_.slice(v[t]);
+                std::copy(sl.table.begin(), sl.table.end(), staging_.begin() + (t - j) * nbk);
+            }
+            dev_upload_async(pool_.slice(v[j])->table_dev, staging_.data(), staging_.size() * sizeof(int32_t),
+                             stream_);
+            dev_stream_sync(stream_);    // staging_ is reused by the next run
+            j = e;
+        }
+    }
 
     // session_attach (session.h:156-163)
     void attach(KvSlice& dst, const KvSlice& src, int k) {
@@ -172,6 +233,7 @@ private:
     int32_t* tables_ = nullptr;
     uint64_t pool_bytes_ = 0;
     nova_stream_t stream_ = nullptr;
+    std::vector<int32_t> staging_;
 };
 
 }  // namespace nova

@@ -138,6 +138,8 @@ _SIGS = {
     "nova_paged_cow_guard": (i32, [vp, i32, i64, vp]),
     "nova_paged_session_cow": (None, [vp, i32, i64, i32, vp]),
     "nova_paged_cow_batch": (i32, [vp, P_int, P_i64, P_int, i32, vp]),
+    "nova_paged_create_sessions": (i32, [vp, i32, i32, P_int]),
+    "nova_paged_push_tables": (None, [vp, P_int, i32]),
     "nova_paged_table_dev": (vp, [vp, i32]),
 }
 

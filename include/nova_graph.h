@@ -83,6 +83,15 @@ void          nova_paged_session_cow(nova_paged_t h, int s, int64_t pos0, int n,
 int           nova_paged_cow_batch(nova_paged_t h, const int* sessions, const int64_t* pos0, const int* n,
                                    int count, nova_stream_t st);
 int32_t*      nova_paged_table_dev(nova_paged_t h, int s);
+/* Batched session manager (no single counterpart in the reference: it
+ * replaces N calls of SessionManager::create's paging steps, session.h:84-142,
+ * and N table uploads).  create_sessions acquires `count` slices in the order
+ * serial creates would (ids out, -1 past pool exhaustion; returns the number
+ * created), uploads their tables with one copy per run of consecutive ids and
+ * clears all their pages in one launch.  push_tables re-uploads the host
+ * tables of `count` sessions the same way. */
+int           nova_paged_create_sessions(nova_paged_t h, int count, int clear_pages, int* ids);
+void          nova_paged_push_tables(nova_paged_t h, const int* ids, int count);
 
 #ifdef __cplusplus
 }

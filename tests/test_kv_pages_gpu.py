@@ -152,3 +152,62 @@ def free_of(nova, pool):
     buf = (C.c_int * max(n, 1))()
     nova.nova_kvpool_free_list(pool, buf, n)
     return list(buf[:n])
+
+
+def test_batched_session_manager(nova7, oracle):
+    """create_sessions / push_tables: the ids serial creates would give (oracle
+    pool driven with the same acquire/release sequence), exhaustion reported
+    as -1, every created session's pages cleared and no other page touched,
+    device tables equal to the host tables after host-side attaches pushed in
+    one call."""
+    nova = nova7
+    print("[case] batched session manager", flush=True)
+    ctx = 64
+    h = nova.nova_paged_new(8, ctx)
+    try:
+        pool = nova.nova_paged_pool(h)
+        o = oracle.pool
+        oh = o.new(8, ctx)
+        nb = nova.nova_paged_nb(h)
+        kp, vp = nova.nova_paged_pool_k(h), nova.nova_paged_pool_v(h)
+        shape = (nova.n_layers, nb, nova.kb, nova.nkv, nova.hd)
+        per = nova.n_layers * nb * nova.kb * nova.kvw
+        first = [nova.nova_paged_create_session(h, 0) for _ in range(3)]
+        assert first == [o.acquire(oh) for _ in range(3)]
+        nova.nova_paged_destroy_session(h, first[1])
+        o.release(oh, first[1])
+        nova.testkit_fill_normal_f16(kp, per, 11, 1.0, None)
+        nova.testkit_fill_normal_f16(vp, per, 12, 1.0, None)
+        nova.dev_sync()
+        before_k = nova.download(kp, shape, np.uint16)
+        ids = (C.c_int * 7)()
+        made = nova.nova_paged_create_sessions(h, 7, 1, ids)
+        want = [o.acquire(oh) for _ in range(7)]
+        assert made == 6 and list(ids) == [w if w >= 0 else -1 for w in want] and ids[6] == -1
+        after_k = nova.download(kp, shape, np.uint16)
+        after_v = nova.download(vp, shape, np.uint16)
+        cleared = np.zeros(nb, bool)
+        for s in list(ids)[:made]:
+            cleared[table_of(nova, pool, s)] = True
+        assert not after_k[:, cleared].any() and not after_v[:, cleared].any()
+        assert np.array_equal(after_k[:, ~cleared], before_k[:, ~cleared])
+        live = [first[0], first[2]] + list(ids)[:made]
+        for s in live:
+            dev = nova.download(nova.nova_paged_table_dev(h, s), (ctx // 16,), np.int32)
+            assert dev.tolist() == table_of(nova, pool, s) == o.table_arr(oh, s)
+        # host-only attaches (KvPool), then one batched push
+        kpool = nova.nova_paged_pool(h)
+        targets = list(ids)[:3]
+        for t, n_tok in zip(targets, (17, 33, 64)):
+            nova.nova_kvpool_attach_prefix(kpool, t, first[0], n_tok)
+            o.attach_prefix(oh, t, first[0], n_tok)
+        stale = nova.download(nova.nova_paged_table_dev(h, targets[0]), (ctx // 16,), np.int32).tolist()
+        assert stale != table_of(nova, pool, targets[0])
+        arr = (C.c_int * 3)(targets[2], targets[0], targets[1])
+        nova.nova_paged_push_tables(h, arr, 3)
+        for s in live:
+            dev = nova.download(nova.nova_paged_table_dev(h, s), (ctx // 16,), np.int32)
+            assert dev.tolist() == o.table_arr(oh, s)
+        o.delete(oh)
+    finally:
+        nova.nova_paged_delete(h)

@@ -184,6 +184,16 @@ void launch_quant_q8(int8_t* qs, float* d, int32_t* sums, const float* x, int ro
  * types.h:17-21, passed here as plain arguments). */
 void launch_gemv_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_t* xq, const float* xd,
                      const int32_t* xs, float* out, nova_stream_t s);
+/* The quantisation and the GEMVs that share one activation in one launch:
+ * n_mat (1..4) Q4_K matrices of the same width cols (blocks[m], rows[m],
+ * outs[m]; host arrays) against fp32 x, quantised inside the launch with the
+ * arithmetic of launch_quant_q8 (same codes, scales and sums, so outs[m] is
+ * bit-identical to launch_quant_q8 followed by launch_gemv_q4k per matrix).
+ * Replaces the reference's Kernel::quant (include/nova/kernel.h:80-86,
+ * kernel q4k_gemv.cu:9-33) followed by gemm_q4k/launch_gemv for each of the
+ * q/k/v or gate/up projections (kernel.h:29-34, q4k_gemv.cu:209-213). */
+void launch_gemv_q4k_f32(const uint8_t* const* blocks, const int64_t* rows, float* const* outs, int n_mat,
+                         int cols, const float* x, nova_stream_t s);
 
 #ifdef __cplusplus
 }

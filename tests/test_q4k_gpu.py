@@ -69,3 +69,44 @@ def test_gemv_matches_oracle(rows, cols, nova7, oracle):
     assert np.all(np.isfinite(got))
     assert np.all(err <= 2e-6 * scale), f"max err/scale {np.max(err / scale):.2e}"
     print(f"  max |gpu-oracle| / sum|terms| = {np.max(err / scale):.2e}")
+
+
+@pytest.mark.parametrize("cols,rows", [(3584, (37, 0, 512)), (3584, (3584,)), (18944, (130, 61)), (256, (5, 1, 2, 9)),
+                                       (8960, (33, 70)), (32768, (3, 4))])
+def test_gemv_f32_fused(cols, rows, nova7, oracle):
+    """launch_gemv_q4k_f32 (quantise inside the launch, up to 4 matrices over one
+    activation) equals launch_quant_q8 + launch_gemv_q4k per matrix bit for
+    bit, and the oracle within the GEMV tolerance."""
+    import ctypes as C
+    nova = nova7
+    print(f"[case] gemv f32 fused cols={cols} rows={rows}", flush=True)
+    rng = np.random.default_rng(cols + sum(rows))
+    ws = [random_blocks(rng, r, cols) for r in rows]
+    x = (rng.standard_normal((1, cols)) * rng.uniform(0.1, 8.0)).astype(np.float32)
+    x[0, 64:96] = 0.0                                      # an all-zero 32-block: d = 0
+    dx = nova.upload(x)
+    dws = [nova.upload(w) if w.size else nova.alloc(16) for w in ws]
+    fused = [nova.upload(np.full(max(r, 1), np.nan, np.float32)) for r in rows]
+    sep = [nova.upload(np.full(max(r, 1), np.nan, np.float32)) for r in rows]
+    n = len(rows)
+    bl = (C.c_void_p * n)(*[d.ptr for d in dws])
+    rw = (C.c_int64 * n)(*rows)
+    ou = (C.c_void_p * n)(*[o.ptr for o in fused])
+    nova.launch_gemv_q4k_f32(bl, rw, ou, n, cols, dx.ptr, None)
+    qs, dd, ss = nova.alloc(cols), nova.alloc(cols // 8), nova.alloc(cols // 4)
+    nova.launch_quant_q8(qs.ptr, dd.ptr, ss.ptr, dx.ptr, 1, cols, None)
+    for m, r in enumerate(rows):
+        nova.launch_gemv_q4k(dws[m].ptr, r, cols, qs.ptr, dd.ptr, ss.ptr, sep[m].ptr, None)
+    nova.dev_sync()
+    oq, od, os_ = oracle.quant_q8(x)
+    for m, r in enumerate(rows):
+        if r == 0:
+            assert np.isnan(fused[m].numpy((1,), np.float32)[0])       # nothing written
+            continue
+        got = fused[m].numpy((r,), np.float32)
+        assert np.array_equal(got.view(np.uint32), sep[m].numpy((r,), np.float32).view(np.uint32)), m
+        check = slice(None) if r <= 600 else slice(0, r, max(r // 300, 1))
+        ref = oracle.gemv_q4k(ws[m], r, cols, oq, od, os_)
+        scale = abs_terms(oracle, ws[m][check], len(range(r)[check]), cols, oq, od)
+        err = np.abs(got[check].astype(np.float64) - ref[check])
+        assert np.all(err <= 2e-6 * scale), f"matrix {m}: max err/scale {np.max(err / scale):.2e}"

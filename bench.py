@@ -175,6 +175,58 @@ class DecodeWorkload:
                 cnt += 1
         return total / cnt
 
+    def rope_compare(self, steps, warmup):
+        """The decode step with RoPE in front of it (a real model's step): the
+        separate launch_rope_kv_store_paged_batch + planned decode per layer,
+        against launch_attn_decode_paged_rope_planned (one launch pair per
+        layer).  Both from HIP graphs; us per step for each."""
+        nv, s, L = self.nova, self.s, self.layers
+        rows = int(self.n_keys.max())
+        half = nv.hd // 2
+        cs, sn = nv.alloc(rows * half * 4), nv.alloc(rows * half * 4)
+        nv.launch_rope_table_rows(cs.ptr, sn.ptr, rows, s)
+        rng = np.random.default_rng(5)
+        k32 = nv.upload(rng.standard_normal((L, self.n, nv.nkv, nv.hd)).astype(np.float32))
+        v32 = nv.upload(rng.standard_normal((L, self.n, nv.nkv, nv.hd)).astype(np.float32))
+        qsep = nv.upload(self.q_h)
+        pos = nv.upload(self.ctx)
+        qs, kvs = self.n * nv.nh * nv.hd, self.n * nv.kvw
+
+        def separate():
+            self.plan()
+            for l in range(L):
+                nv.launch_rope_kv_store_paged_batch(qsep.ptr + l * qs * 4, k32.ptr + l * kvs * 4,
+                                                    v32.ptr + l * kvs * 4, cs.ptr, sn.ptr, self.k.ptr, self.v.ptr,
+                                                    self.tables.ptr, self.max_pages, pos.ptr, self.n, 1, l,
+                                                    self.nb, s)
+                nv.launch_attn_decode_paged_planned(qsep.ptr + l * qs * 4, self.k.ptr, self.v.ptr, self.tables.ptr,
+                                                    self.max_pages, self.n, l, self.nb, None, None,
+                                                    self.o.ptr + l * qs * 4, self.ws.ptr, s)
+
+        def fused():
+            self.plan()
+            for l in range(L):
+                nv.launch_attn_decode_paged_rope_planned(self.q.ptr + l * qs * 4, k32.ptr + l * kvs * 4,
+                                                         v32.ptr + l * kvs * 4, cs.ptr, sn.ptr, self.k.ptr,
+                                                         self.v.ptr, self.tables.ptr, self.max_pages, self.n, l,
+                                                         self.nb, self.o.ptr + l * qs * 4, self.ws.ptr, s)
+
+        out = {}
+        for name, fn in (("separate_us_per_step", separate), ("fused_us_per_step", fused)):
+            nv.dev_graph_begin(s)
+            fn()
+            g = nv.dev_graph_end(s)
+            for _ in range(warmup):
+                nv.dev_graph_launch(g, s)
+            t = Timer(nv, s)
+            t.start()
+            for _ in range(steps):
+                nv.dev_graph_launch(g, s)
+            out[name] = round(t.stop() / steps * 1e3, 2)
+            nv.dev_graph_destroy(g)
+        nv.dev_stream_sync(s)
+        return out
+
     def cpu_sample(self, layer, threads):
         """Run the C oracle on the host over one layer; returns (seconds, outputs)."""
         from oracle_py import Oracle
@@ -230,6 +282,7 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
     bytes_step = wl.bytes_per_step()
     gbs = bytes_step / (ms * 1e-3) / 1e9
     k_ms = wl.kernel_ms()
+    rope = wl.rope_compare(args.steps, args.warmup) if model == "qwen25_7b" else None
     bytes_launch = bytes_step / wl.layers
     achieved = bytes_launch / (k_ms * 1e-3) / 1e9
     traffic = load_traffic(workload_name)
@@ -257,6 +310,11 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
         "data": "synthetic (seeded N(0,1) K/V, Q; seeded ragged contexts and page shuffle)",
         "config": metric_cfg["config"], "roofline": roof, "cpu_baseline": cpu,
     }
+    if rope:
+        line["rope_in_step"] = dict(rope, note="the same step with RoPE of q and the new k in front of each layer: "
+                                               "launch_rope_kv_store_paged_batch + planned decode, against "
+                                               "launch_attn_decode_paged_rope_planned (RoPE and append inside the "
+                                               "decode launch)")
     return line
 
 

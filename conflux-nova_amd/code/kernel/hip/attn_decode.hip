@@ -55,6 +55,7 @@
 #include "check.h"
 #include "model.h"
 #include "nova_kernel.h"
+#include "rope_math.h"
 
 namespace nova {
 namespace {
@@ -90,6 +91,10 @@ struct DecodeArgs {
     int nb;
     const uint16_t* k_new;   // [n_sess][NKV][HD] or null
     const uint16_t* v_new;
+    const float* k_new32;    // fused RoPE: new token fp32 [n_sess][NKV][HD], rotated here
+    const float* v_new32;
+    const float* cs;         // RoPE table rows [pos][HD/2] (null: no rotation)
+    const float* sn;
     float* part;             // [(Gw + n_sess)][NH][PW]
     const int32_t* plan;     // per-step plan (null: derive the partition in-kernel)
     int gw;                  // workgroups in the grid
@@ -190,6 +195,7 @@ struct PairRegs {
     u4 v[8];           // V rows kappa(g,j) = (page j/4, slot 4g + j%4), halves [8c, +8)
 };
 
+template <bool kRope>
 __global__ void __launch_bounds__(THREADS)
 decode_split_kernel(DecodeArgs a) {
     __shared__ float s_m[WAVES][16];
@@ -278,7 +284,7 @@ decode_split_kernel(DecodeArgs a) {
 
         // The first pair's loads go out now, together with the Q loads below,
         // unless the fused append is about to write into it (then after the barrier).
-        const bool appends = a.k_new && pb == last_page + 1;
+        const bool appends = (kRope || a.k_new) && pb == last_page + 1;
         const bool early = !(appends && pa + 2 * r + 1 >= last_page);
         PairRegs cur;
         if (r < npairs && early) load_pair(r, cur);
@@ -289,11 +295,30 @@ decode_split_kernel(DecodeArgs a) {
             const int phys = table[last_page];
             const int64_t dst = ((layer_page0 + phys) * kPageBytes + (int64_t)((n_keys - 1) & kKvBlockMask) * kRowBytes) / 2;
             const int64_t src = (int64_t)i * KVW;
-            for (int e = tid; e < KVW / 8; e += THREADS) {
-                *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_k) + dst + 8 * e) =
-                    *reinterpret_cast<const u4*>(a.k_new + src + 8 * e);
-                *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_v) + dst + 8 * e) =
-                    *reinterpret_cast<const u4*>(a.v_new + src + 8 * e);
+            if constexpr (kRope) {
+                // RopeKvOp (code/graph/dense.h:75-83): k rotated at position
+                // n_keys - 1, k and v rounded to fp16 (nearest even)
+                uint16_t* pk16 = const_cast<uint16_t*>(a.pool_k) + dst;
+                uint16_t* pv16 = const_cast<uint16_t*>(a.pool_v) + dst;
+                const float* crow = a.cs + (int64_t)(n_keys - 1) * (HD / 2);
+                const float* srow = a.sn + (int64_t)(n_keys - 1) * (HD / 2);
+                for (int e = tid; e < NKV * (HD / 2); e += THREADS) {
+                    const int h = e / (HD / 2), d = e - h * (HD / 2);
+                    const float* kr = a.k_new32 + src + h * HD;
+                    float y0, y1;
+                    rope_rotate(kr[d], kr[d + HD / 2], crow[d], srow[d], y0, y1);
+                    pk16[h * HD + d] = __builtin_bit_cast(uint16_t, (_Float16)y0);
+                    pk16[h * HD + d + HD / 2] = __builtin_bit_cast(uint16_t, (_Float16)y1);
+                }
+                for (int e = tid; e < KVW; e += THREADS)
+                    pv16[e] = __builtin_bit_cast(uint16_t, (_Float16)a.v_new32[src + e]);
+            } else {
+                for (int e = tid; e < KVW / 8; e += THREADS) {
+                    *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_k) + dst + 8 * e) =
+                        *reinterpret_cast<const u4*>(a.k_new + src + 8 * e);
+                    *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_v) + dst + 8 * e) =
+                        *reinterpret_cast<const u4*>(a.v_new + src + 8 * e);
+                }
             }
         }
 
@@ -314,6 +339,26 @@ decode_split_kernel(DecodeArgs a) {
                     qv[ks][jj] = real ? x0[jj] : 0.f;
                     qv[ks][4 + jj] = real ? x1[jj] : 0.f;
                 }
+            }
+            if constexpr (kRope) {
+                // RoPE of q at position n_keys - 1: lane (g,c) holds dims
+                // 32ks + 8g + jj, so the pair (d, d + 64) is (ks, ks + 2) in
+                // the same lane; the caller's q is left as it is
+                const float* crow = a.cs + (int64_t)(n_keys - 1) * (HD / 2) + 8 * g;
+                const float* srow = a.sn + (int64_t)(n_keys - 1) * (HD / 2) + 8 * g;
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                    for (int jj = 0; jj < 8; ++jj) {
+                        float y0, y1;
+                        rope_rotate(qv[ks][jj], qv[ks + 2][jj], crow[32 * ks + jj], srow[32 * ks + jj], y0, y1);
+                        qv[ks][jj] = y0;
+                        qv[ks + 2][jj] = y1;
+                    }
+                }
+            }
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) amax = fmaxf(amax, fabsf(qv[ks][jj]));
             }
@@ -640,7 +685,8 @@ int batch_workgroups() {
 }
 
 void launch_pair(const DecodeArgs& a, int n_sess, float* o, hipStream_t st) {
-    hipLaunchKernelGGL(decode_split_kernel, dim3(a.gw + n_sess), dim3(THREADS), 0, st, a);
+    if (a.cs) hipLaunchKernelGGL(decode_split_kernel<true>, dim3(a.gw + n_sess), dim3(THREADS), 0, st, a);
+    else hipLaunchKernelGGL(decode_split_kernel<false>, dim3(a.gw + n_sess), dim3(THREADS), 0, st, a);
     NOVA_LAUNCHED();
     hipLaunchKernelGGL(decode_combine_kernel, dim3(n_sess, NKV), dim3(CT), 0, st, a, o);
     NOVA_LAUNCHED();
@@ -700,6 +746,35 @@ void launch_attn_decode_paged_planned(const float* q, uint16_t* pool_k, uint16_t
     a.k_new = k_new;
     a.v_new = v_new;
     launch_pair(a, n_sess, o, reinterpret_cast<hipStream_t>(s));
+}
+
+void launch_attn_decode_paged_rope_planned(const float* q, const float* k_new, const float* v_new, const float* cs,
+                                           const float* sn, uint16_t* pool_k, uint16_t* pool_v,
+                                           const int32_t* tables, int table_stride, int n_sess, int layer, int nb,
+                                           float* o, void* workspace, nova_stream_t s) {
+    NOVA_REQUIRE(q && k_new && v_new && cs && sn && pool_k && pool_v && o);
+    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0);
+    DecodeArgs a = batch_args(tables, table_stride, nullptr, n_sess, workspace);
+    a.q = q;
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.layer = layer;
+    a.nb = nb;
+    a.k_new32 = k_new;
+    a.v_new32 = v_new;
+    a.cs = cs;
+    a.sn = sn;
+    launch_pair(a, n_sess, o, reinterpret_cast<hipStream_t>(s));
+}
+
+void launch_attn_decode_paged_rope_batch(const float* q, const float* k_new, const float* v_new, const float* cs,
+                                         const float* sn, uint16_t* pool_k, uint16_t* pool_v,
+                                         const int32_t* tables, int table_stride, const int32_t* n_keys,
+                                         int n_sess, int layer, int nb, float* o, void* workspace,
+                                         nova_stream_t s) {
+    launch_attn_decode_plan(tables, table_stride, n_keys, n_sess, workspace, s);
+    launch_attn_decode_paged_rope_planned(q, k_new, v_new, cs, sn, pool_k, pool_v, tables, table_stride, n_sess,
+                                          layer, nb, o, workspace, s);
 }
 
 void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* pool_v,

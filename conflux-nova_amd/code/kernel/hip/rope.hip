@@ -27,6 +27,7 @@
 #include "check.h"
 #include "model.h"
 #include "nova_kernel.h"
+#include "rope_math.h"
 
 namespace nova {
 namespace {
@@ -56,17 +57,14 @@ __global__ void rope_table_kernel(float* __restrict__ cs, float* __restrict__ sn
     sn[idx] = (float)sin((double)a);
 }
 
-// x0*c - x1*s and x0*s + x1*c with every product rounded: the products pass
-// through an empty asm so that they cannot be contracted into an fma (the
-// library is built with -ffp-contract=fast, under which clang ignores the
-// fp-contract pragma)
+// four pairs at once, each through rope_rotate (every product rounded, no fma)
 __device__ __forceinline__ void rotate(const f4 x0, const f4 x1, const f4 c, const f4 s, f4& y0, f4& y1) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        float a0 = x0[e] * c[e], a1 = x1[e] * s[e], b0 = x0[e] * s[e], b1 = x1[e] * c[e];
-        asm("" : "+v"(a0), "+v"(a1), "+v"(b0), "+v"(b1));
-        y0[e] = a0 - a1;
-        y1[e] = b0 + b1;
+        float a, b;
+        rope_rotate(x0[e], x1[e], c[e], s[e], a, b);
+        y0[e] = a;
+        y1[e] = b;
     }
 }
 

@@ -69,6 +69,8 @@ _SIGS = {
     "launch_attn_decode_paged": (None, [vp, vp, vp, vp, i32, i32, i32, vp, vp, vp]),
     "launch_attn_prefill_paged": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "attn_decode_batch_workspace_bytes": (sz, [i32]),
+    "launch_attn_decode_paged_rope_planned": (None, [vp, vp, vp, vp, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp]),
+    "launch_attn_decode_paged_rope_batch": (None, [vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp]),
     "launch_attn_decode_paged_batch": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp, vp, vp]),
     "launch_attn_decode_plan": (None, [vp, i32, vp, i32, vp, vp]),
     "launch_attn_decode_paged_planned": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]),

@@ -92,6 +92,25 @@ void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* 
                                     int n_sess, int layer, int nb,
                                     const uint16_t* k_new, const uint16_t* v_new,
                                     float* o, void* workspace, nova_stream_t s);
+/* The batched decode with the step before it fused in: RopeKvOp
+ * (code/graph/dense.h:75-83: rope_batch of q and k at position n_keys[i]-1,
+ * src/kernel/rope.cu:21-58, then kv_store_paged of k and v) and the
+ * attention of the planned call above, in one launch pair.  k_new, v_new:
+ * the layer's new token, fp32 [n_sess][NKV][HD], unrotated; k is rotated with
+ * the cs/sn table rows of launch_rope_table (every row used must exist) and
+ * written with v as fp16 (nearest even) into the session's last page; q is
+ * rotated in registers as it is loaded and the caller's q is not modified.
+ * The appended rows are bit-identical to launch_rope_kv_store_paged_batch's;
+ * n_keys[i] counts the new token and must be >= 1 for every session. */
+void launch_attn_decode_paged_rope_planned(const float* q, const float* k_new, const float* v_new, const float* cs,
+                                           const float* sn, uint16_t* pool_k, uint16_t* pool_v,
+                                           const int32_t* tables, int table_stride, int n_sess, int layer, int nb,
+                                           float* o, void* workspace, nova_stream_t s);
+void launch_attn_decode_paged_rope_batch(const float* q, const float* k_new, const float* v_new, const float* cs,
+                                         const float* sn, uint16_t* pool_k, uint16_t* pool_v,
+                                         const int32_t* tables, int table_stride, const int32_t* n_keys,
+                                         int n_sess, int layer, int nb, float* o, void* workspace,
+                                         nova_stream_t s);
 
 /* Batched append: session i writes n tokens at positions pos0[i]..pos0[i]+n-1
  * (pos0: device int32[n_sess]) through tables + i*table_stride; k, v:

@@ -181,3 +181,56 @@ def test_decode_batch_many_sessions(nova7, oracle):
                                        int(n_keys[i]))
         worst = max(worst, assert_close(got[i], ref, what=f"session {i} n_keys={n_keys[i]}"))
     print(f"  worst max|gpu-oracle|={worst:.3e}")
+
+
+@pytest.mark.parametrize("model", ["qwen25_7b", "qwen25_1p5b", "qwen25_14b"])
+def test_decode_batch_rope_fused(model, oracle):
+    """launch_attn_decode_paged_rope_batch = RopeKvOp (rope of q and k at
+    n_keys-1, fp16 append of k and v) + the batched decode: appended rows
+    bit-exact against or_rope_kv_store_paged, the output within tolerance of
+    the oracle's decode over the rotated q, the caller's q untouched, and the
+    rotation really applied (the unrotated result differs)."""
+    import nova_amd
+    nova = nova_amd.load(model)
+    rng = np.random.default_rng(23)
+    n_sess = 16
+    n_keys = rng.integers(1, 900, n_sess).astype(np.int32)
+    n_keys[2], n_keys[7], n_keys[9] = 1, 16, 17
+    max_pages = int((n_keys.max() + 15) // 16)
+    print(f"[case] decode batch rope fused model={model} n_keys={n_keys.tolist()}", flush=True)
+    fx = PagedFixture(nova, nb=n_sess * max_pages + 5, layer=LAYER, seed=8)
+    tables = fx.tables(n_sess, max_pages)
+    half = nova.hd // 2
+    dcs, dsn = nova.alloc(4096 * half * 4), nova.alloc(4096 * half * 4)
+    nova.launch_rope_table(dcs.ptr, dsn.ptr, None)
+    nova.dev_sync()
+    cs, sn = dcs.numpy((4096, half), np.float32), dsn.numpy((4096, half), np.float32)
+    q = rng.standard_normal((n_sess, nova.nh, nova.hd)).astype(np.float32)
+    k = rng.standard_normal((n_sess, nova.nkv, nova.hd)).astype(np.float32)
+    v = rng.standard_normal((n_sess, nova.nkv, nova.hd)).astype(np.float32)
+    ws = nova.alloc(nova.attn_decode_batch_workspace_bytes(n_sess))
+    dq, dk, dv = nova.upload(q), nova.upload(k), nova.upload(v)
+    dt, dn = nova.upload(tables), nova.upload(n_keys)
+    do = nova.alloc(q.nbytes)
+    nova.launch_attn_decode_paged_rope_batch(dq.ptr, dk.ptr, dv.ptr, dcs.ptr, dsn.ptr, fx.k.ptr, fx.v.ptr, dt.ptr,
+                                             max_pages, dn.ptr, n_sess, LAYER, fx.nb, do.ptr, ws.ptr, None)
+    nova.dev_sync()
+    got = do.numpy(q.shape, np.float32)
+    assert np.array_equal(dq.numpy(q.shape, np.float32), q), "caller's q modified"
+    hk, hv = fx.hk.copy(), fx.hv.copy()
+    rqs = []
+    for i in range(n_sess):
+        rqs.append(oracle.rope_kv_store_paged(model, q[i][None], k[i][None], v[i][None], cs, sn, hk, hv,
+                                              np.ascontiguousarray(tables[i]), 0, fx.nb, int(n_keys[i]) - 1)[0])
+    gk, gv = fx.pull()
+    assert np.array_equal(gk, hk) and np.array_equal(gv, hv), "fused rope + append not bit-exact"
+    worst = 0.0
+    for i in range(n_sess):
+        ref = oracle.attn_decode_paged(model, np.ascontiguousarray(rqs[i]), hk, hv, tables[i], 0, fx.nb,
+                                       int(n_keys[i]))
+        worst = max(worst, assert_close(got[i], ref, what=f"session {i} n_keys={n_keys[i]}"))
+        if n_keys[i] > 1:
+            plain = oracle.attn_decode_paged(model, np.ascontiguousarray(q[i]), hk, hv, tables[i], 0, fx.nb,
+                                             int(n_keys[i]))
+            assert np.abs(plain - ref).max() > 1e-3, "rotation had no effect"
+    print(f"  worst max|gpu-oracle|={worst:.3e}")

@@ -75,6 +75,10 @@ def _abort_run(code):
     ("n.launch_gemv_q4k(1, 4, 300, 1, 1, 1, 1, None)", "cols % kQK == 0"),
     ("n.launch_gemv_q4k(1, 4, 65536, 1, 1, 1, 1, None)", "cols <= kMaxCols"),
     ("n.launch_quant_q8(1, 1, 1, 1, 1, 33, None)", "cols % 32 == 0"),
+    ("n.launch_attn_decode_paged_rope_planned(1, 1, 1, None, 1, 1, 1, 1, 1, 1, 0, 4, 1, 1, None)",
+     "q && k_new && v_new && cs && sn"),
+    ("n.launch_attn_decode_paged_rope_planned(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 28, 4, 1, 1, None)",
+     "layer < Model::L"),
     ("import ctypes as C; n.launch_gemv_q4k_f32((C.c_void_p * 5)(*[1] * 5), (C.c_int64 * 5)(*[1] * 5), "
      "(C.c_void_p * 5)(*[1] * 5), 5, 256, 1, None)", "n_mat <= kMaxMats"),
     ("import ctypes as C; n.launch_gemv_q4k_f32((C.c_void_p * 1)(1), (C.c_int64 * 1)(1), (C.c_void_p * 1)(1), "

@@ -27,6 +27,7 @@
 //    reference's; the row sum is a wave reduction.
 #include <hip/hip_runtime.h>
 #include <cstdint>
+#include <mutex>
 
 #include "check.h"
 #include "nova_kernel.h"
@@ -112,18 +113,23 @@ __device__ __forceinline__ void scale_min(int j, const uint32_t sw[3], uint32_t&
     }
 }
 
-// one lane's share of super-block sb (header hd, nibbles nb16) against the
-// activation staged in LDS: the two sub-block terms of the reference's sum
-__device__ __forceinline__ float sb_terms(const u4 hd, const u4 nb16, int sb, int grp, int elo,
-                                          const int8_t* s_q, const float* s_d, const int32_t* s_s) {
-    const int k0 = sb * kQK + elo;             // low-nibble elements k0..k0+15, high k0+32..
-    const i4 alo = *reinterpret_cast<const i4*>(s_q + k0);
-    const i4 ahi = *reinterpret_cast<const i4*>(s_q + k0 + 32);
-    int dlo = 0, dhi = 0;
+// One lane's share of a super-block, split in two so that several
+// activations can reuse one weight load: sb_prep unpacks the lane's 16 nibble
+// bytes (16 weights of sub-block 2grp in the low nibbles, 16 of 2grp+1 in the
+// high) and the two (d*scale, dmin*min) pairs; sb_dot takes the products with
+// one activation staged in LDS (codes, scales per 32, sums per 16).  The
+// float combination is the reference's: dx * (d*sc*sum(q*c) - dmin*m*sum(c)).
+struct SbW {
+    int lo[4], hi[4];          // nibbles as int8 lanes for v_dot4_i32_i8
+    float al, bl, ah, bh;      // d*sc and dmin*m of the two sub-blocks
+};
+
+__device__ __forceinline__ SbW sb_prep(const u4 hd, const u4 nb16, int grp) {
+    SbW w;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-        dlo = __builtin_amdgcn_sdot4((int)(nb16[e] & 0x0F0F0F0Fu), alo[e], dlo, false);
-        dhi = __builtin_amdgcn_sdot4((int)((nb16[e] >> 4) & 0x0F0F0F0Fu), ahi[e], dhi, false);
+        w.lo[e] = (int)(nb16[e] & 0x0F0F0F0Fu);
+        w.hi[e] = (int)((nb16[e] >> 4) & 0x0F0F0F0Fu);
     }
     const uint32_t sw[3] = {hd[1], hd[2], hd[3]};
     uint32_t scl, mcl, sch, mch;
@@ -131,10 +137,32 @@ __device__ __forceinline__ float sb_terms(const u4 hd, const u4 nb16, int sb, in
     scale_min(2 * grp + 1, sw, sch, mch);
     const float dd = half_to_float(hd[0] & 0xFFFFu);
     const float dm = half_to_float(hd[0] >> 16);
+    w.al = dd * (float)scl;
+    w.bl = dm * (float)mcl;
+    w.ah = dd * (float)sch;
+    w.bh = dm * (float)mch;
+    return w;
+}
+
+// k0: the lane's first element (low nibbles) in the row; high nibbles at k0 + 32
+__device__ __forceinline__ float sb_dot(const SbW& w, int k0, const int8_t* s_q, const float* s_d,
+                                        const int32_t* s_s) {
+    const i4 alo = *reinterpret_cast<const i4*>(s_q + k0);
+    const i4 ahi = *reinterpret_cast<const i4*>(s_q + k0 + 32);
+    int dlo = 0, dhi = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        dlo = __builtin_amdgcn_sdot4(w.lo[e], alo[e], dlo, false);
+        dhi = __builtin_amdgcn_sdot4(w.hi[e], ahi[e], dhi, false);
+    }
     const float dxl = s_d[k0 >> 5], dxh = s_d[(k0 + 32) >> 5];
     const int sml = s_s[k0 >> 4], smh = s_s[(k0 + 32) >> 4];
-    return dxl * ((dd * (float)scl) * (float)dlo - (dm * (float)mcl) * (float)sml) +
-           dxh * ((dd * (float)sch) * (float)dhi - (dm * (float)mch) * (float)smh);
+    return dxl * (w.al * (float)dlo - w.bl * (float)sml) + dxh * (w.ah * (float)dhi - w.bh * (float)smh);
+}
+
+__device__ __forceinline__ float sb_terms(const u4 hd, const u4 nb16, int sb, int grp, int elo,
+                                          const int8_t* s_q, const float* s_d, const int32_t* s_s) {
+    return sb_dot(sb_prep(hd, nb16, grp), sb * kQK + elo, s_q, s_d, s_s);
 }
 
 // Up to 4 matrices of the same width that read one activation (q/k/v,
@@ -296,17 +324,106 @@ __global__ void __launch_bounds__(QT) gemv_split_kernel(GemvSet g) {
     }
 }
 
+// Four tokens at once (the reference's gemv4_kernel, q4k_gemv.cu:98-180, as
+// Engine::decode_batch uses it for every projection, model.cpp:270-311):
+// each weight load and its scale unpacking serve four activations.  The four
+// activations (4 x 1.375 B per column) sit in LDS, 104 KB at the FFN width,
+// so a workgroup is 16 waves to keep the CU's waves up.  Rows map to waves
+// exactly as in the one-token kernels (STEPS, KS), and every token's
+// arithmetic is theirs: each output equals launch_gemv_q4k's for that token.
+constexpr int kTok4 = 4;
+constexpr int QT4 = 1024;                      // threads per workgroup
+constexpr int kMaxCols4 = 28672;               // 4 activations within 160 KB of LDS
+
+template <int STEPS, int KS>
+__global__ void __launch_bounds__(QT4) gemv4_kernel(const uint8_t* __restrict__ w, int64_t rows, int cols,
+                                                     const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                     const int32_t* __restrict__ xs, float* __restrict__ out) {
+    extern __shared__ __attribute__((aligned(16))) unsigned char s_x[];
+    __shared__ float s_part[QT4 / 64][kTok4];
+    int8_t* s_q = reinterpret_cast<int8_t*>(s_x);                                   // [4][cols]
+    float* s_d = reinterpret_cast<float*>(s_x + kTok4 * cols);                       // [4][cols/32]
+    int32_t* s_s = reinterpret_cast<int32_t*>(s_x + kTok4 * cols + 4 * kTok4 * (cols / 32));   // [4][cols/16]
+    for (int i = threadIdx.x; i < kTok4 * cols / 16; i += QT4)
+        *reinterpret_cast<u4*>(s_q + 16 * i) = *reinterpret_cast<const u4*>(xq + 16 * i);
+    for (int i = threadIdx.x; i < kTok4 * cols / 32; i += QT4) s_d[i] = xd[i];
+    for (int i = threadIdx.x; i < kTok4 * cols / 16; i += QT4) s_s[i] = xs[i];
+    __syncthreads();
+
+    constexpr int WAVES4 = QT4 / 64;
+    constexpr int RPI = WAVES4 / KS;           // rows per workgroup iteration
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int part = wave % KS;
+    const int j = lane >> 3, c = lane & 7, grp = c >> 1;
+    const int elo = grp * 64 + (c & 1) * 16;
+    const int nsb = cols / kQK;
+    const int sb0 = 8 * STEPS * part + j;
+    const int64_t row_bytes = (int64_t)nsb * kBlockBytes;
+    const int64_t stride = (int64_t)gridDim.x * RPI;
+
+    for (int64_t base = (int64_t)blockIdx.x * RPI; base < rows; base += stride) {   // uniform per workgroup
+        const int64_t r = base + wave / KS;
+        float acc[kTok4] = {0.f, 0.f, 0.f, 0.f};
+        if (r < rows) {
+            const uint8_t* wr = w + r * row_bytes;
+            u4 hdr[STEPS], nib[STEPS];
+#pragma unroll
+            for (int t = 0; t < STEPS; ++t) {
+                const int sb = sb0 + 8 * t;
+                if (sb < nsb) {
+                    const uint8_t* blk = wr + (int64_t)sb * kBlockBytes;
+                    hdr[t] = *reinterpret_cast<const u4*>(blk);
+                    nib[t] = *reinterpret_cast<const u4*>(blk + 16 + 16 * c);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < STEPS; ++t) {
+                const int sb = sb0 + 8 * t;
+                if (sb < nsb) {
+                    const SbW wv = sb_prep(hdr[t], nib[t], grp);
+#pragma unroll
+                    for (int k = 0; k < kTok4; ++k)
+                        acc[k] += sb_dot(wv, sb * kQK + elo, s_q + k * cols, s_d + k * (cols / 32),
+                                         s_s + k * (cols / 16));
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kTok4; ++k)
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) acc[k] += __shfl_xor(acc[k], o, 64);
+        if constexpr (KS == 1) {
+            if (lane == 0 && r < rows)
+#pragma unroll
+                for (int k = 0; k < kTok4; ++k) out[k * rows + r] = acc[k];
+        } else {
+            if (lane == 0)
+#pragma unroll
+                for (int k = 0; k < kTok4; ++k) s_part[wave][k] = acc[k];
+            __syncthreads();
+            if (part == 0 && lane < kTok4 && r < rows) {
+                float sum = s_part[wave][lane];
+#pragma unroll
+                for (int p = 1; p < KS; ++p) sum += s_part[wave + p][lane];
+                out[lane * rows + r] = sum;
+            }
+            __syncthreads();
+        }
+    }
+}
+
 // Workgroups: one per rows_per_wg rows, but no more than can be resident at
 // once (this kernel's occupancy at this LDS size times the CUs); beyond that
 // the kernels grid-stride, so no second partial round of workgroups forms a
 // tail (measured: gate projection 9.8 -> 9.0 us against a fixed cap of 8
 // workgroups per CU, of which 7 fit).
 template <typename K>
-int gemv_grid(K kernel, int64_t rows, int rows_per_wg, size_t lds) {
+int gemv_grid(K kernel, int64_t rows, int rows_per_wg, size_t lds, int block = QT) {
     int dev = 0, cus = 0, per_cu = 0;
     NOVA_HIP(hipGetDevice(&dev));
     NOVA_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    NOVA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, QT, lds));
+    NOVA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds));
     if (per_cu < 1) per_cu = 1;
     const int64_t want = (rows + rows_per_wg - 1) / rows_per_wg;
     const int64_t cap = (int64_t)per_cu * cus;
@@ -323,6 +440,19 @@ template <int STEPS, bool kF32>
 void launch_split(const GemvSet& g, size_t lds, hipStream_t s) {
     auto k = gemv_split_kernel<STEPS, 4, kF32>;
     hipLaunchKernelGGL(k, dim3((unsigned)gemv_grid(k, g.end[g.n - 1], 1, lds)), dim3(QT), lds, s, g);
+}
+
+template <int STEPS, int KS>
+void launch_gemv4_shape(const uint8_t* blocks, int64_t rows, int cols, const int8_t* xq, const float* xd,
+                        const int32_t* xs, float* out, size_t lds, hipStream_t s) {
+    auto k = gemv4_kernel<STEPS, KS>;
+    static std::once_flag once;                // dynamic LDS beyond 64 KB must be allowed per kernel
+    std::call_once(once, [&] {
+        NOVA_HIP(hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                     (int)(kTok4 * (size_t)kMaxCols4 * 11 / 8)));
+    });
+    hipLaunchKernelGGL(k, dim3((unsigned)gemv_grid(k, rows, (QT4 / 64) / KS, lds, QT4)), dim3(QT4), lds, s, blocks,
+                       rows, cols, xq, xd, xs, out);
 }
 
 template <bool kF32>
@@ -374,6 +504,27 @@ void launch_gemv_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_t
     g.xd = xd;
     g.xs = xs;
     launch_set<false>(g, reinterpret_cast<hipStream_t>(s));
+}
+
+void launch_gemv4_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_t* xq, const float* xd,
+                      const int32_t* xs, float* out, nova_stream_t s) {
+    NOVA_REQUIRE(blocks && xq && xd && xs && out && rows >= 0);
+    NOVA_REQUIRE(cols > 0 && cols % kQK == 0 && cols <= kMaxCols4);
+    if (rows == 0) return;
+    const size_t lds = kTok4 * ((size_t)cols + 4 * (size_t)(cols / 32) + 4 * (size_t)(cols / 16));
+    const hipStream_t st = reinterpret_cast<hipStream_t>(s);
+    switch ((cols / kQK + 7) / 8) {            // the one-token kernels' row shapes
+        case 1: launch_gemv4_shape<1, 1>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
+        case 2: launch_gemv4_shape<2, 1>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
+        case 3: launch_gemv4_shape<3, 1>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
+        case 4: launch_gemv4_shape<4, 1>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
+        case 5: case 6: case 7: case 8: launch_gemv4_shape<2, 4>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
+        case 9: case 10: case 11: case 12:
+            launch_gemv4_shape<3, 4>(blocks, rows, cols, xq, xd, xs, out, lds, st);
+            break;
+        default: launch_gemv4_shape<4, 4>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
+    }
+    NOVA_LAUNCHED();
 }
 
 void launch_gemv_q4k_f32(const uint8_t* const* blocks, const int64_t* rows, float* const* outs, int n_mat,

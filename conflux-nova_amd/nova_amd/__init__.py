@@ -78,6 +78,7 @@ _SIGS = {
     "launch_kv_store_paged_batch": (None, [vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp, vp]),
     "launch_quant_q8": (None, [vp, vp, vp, vp, i32, i32, vp]),
     "launch_gemv_q4k": (None, [vp, i64, i32, vp, vp, vp, vp, vp]),
+    "launch_gemv4_q4k": (None, [vp, i64, i32, vp, vp, vp, vp, vp]),
     "launch_gemv_q4k_f32": (None, [C.POINTER(vp), P_i64, C.POINTER(vp), i32, i32, vp, vp]),
     "launch_rope_table": (None, [vp, vp, vp]),
     "launch_rope_table_rows": (None, [vp, vp, i32, vp]),

@@ -203,6 +203,15 @@ void launch_quant_q8(int8_t* qs, float* d, int32_t* sums, const float* x, int ro
  * types.h:17-21, passed here as plain arguments). */
 void launch_gemv_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_t* xq, const float* xd,
                      const int32_t* xs, float* out, nova_stream_t s);
+/* Four tokens: out[t][r] = row r . activation t for t = 0..3 -- the reference's
+ * launch_gemv4<K, R> (q4k_gemv.cu:182-187, kernel :98-180), which
+ * Engine::decode_batch uses for every projection (model.cpp:270-311).  The
+ * four ActQ8 activations are stacked: xq [4][cols], xd [4][cols/32],
+ * xs [4][cols/16]; out [4][rows].  Each weight is read once for the four
+ * tokens, and out[t] is bit-identical to launch_gemv_q4k on token t.
+ * cols % 256 == 0, cols <= 28672. */
+void launch_gemv4_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_t* xq, const float* xd,
+                      const int32_t* xs, float* out, nova_stream_t s);
 /* The quantisation and the GEMVs that share one activation in one launch:
  * n_mat (1..4) Q4_K matrices of the same width cols (blocks[m], rows[m],
  * outs[m]; host arrays) against fp32 x, quantised inside the launch with the

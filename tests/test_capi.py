@@ -75,6 +75,7 @@ def _abort_run(code):
     ("n.launch_gemv_q4k(1, 4, 300, 1, 1, 1, 1, None)", "cols % kQK == 0"),
     ("n.launch_gemv_q4k(1, 4, 65536, 1, 1, 1, 1, None)", "cols <= kMaxCols"),
     ("n.launch_quant_q8(1, 1, 1, 1, 1, 33, None)", "cols % 32 == 0"),
+    ("n.launch_gemv4_q4k(1, 4, 28928, 1, 1, 1, 1, None)", "cols <= kMaxCols4"),
     ("n.launch_attn_decode_paged_rope_planned(1, 1, 1, None, 1, 1, 1, 1, 1, 1, 0, 4, 1, 1, None)",
      "q && k_new && v_new && cs && sn"),
     ("n.launch_attn_decode_paged_rope_planned(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 28, 4, 1, 1, None)",

@@ -110,3 +110,37 @@ def test_gemv_f32_fused(cols, rows, nova7, oracle):
         scale = abs_terms(oracle, ws[m][check], len(range(r)[check]), cols, oq, od)
         err = np.abs(got[check].astype(np.float64) - ref[check])
         assert np.all(err <= 2e-6 * scale), f"matrix {m}: max err/scale {np.max(err / scale):.2e}"
+
+
+@pytest.mark.parametrize("rows,cols", [(37, 256), (512, 3584), (3584, 3584), (130, 18944), (70, 8960),
+                                       (33, 13824), (5, 28672), (1, 1536)])
+def test_gemv4_matches_single_token(rows, cols, nova7, oracle):
+    """launch_gemv4_q4k (4 stacked tokens, one weight read): every token's
+    output bit-identical to launch_gemv_q4k on that token, and within the
+    GEMV tolerance of the oracle."""
+    nova = nova7
+    print(f"[case] gemv4 rows={rows} cols={cols}", flush=True)
+    rng = np.random.default_rng(rows * 13 + cols)
+    w = random_blocks(rng, rows, cols)
+    x = (rng.standard_normal((4, cols)) * rng.uniform(0.2, 5.0, (4, 1))).astype(np.float32)
+    x[2, :32] = 0.0
+    qs, d, s = oracle.quant_q8(x)
+    dw, dq, dd, ds = nova.upload(w), nova.upload(qs), nova.upload(d), nova.upload(s)
+    out4 = nova.upload(np.full(4 * rows, np.nan, np.float32))
+    nova.launch_gemv4_q4k(dw.ptr, rows, cols, dq.ptr, dd.ptr, ds.ptr, out4.ptr, None)
+    singles = []
+    for t in range(4):
+        o1 = nova.upload(np.full(rows, np.nan, np.float32))
+        nova.launch_gemv_q4k(dw.ptr, rows, cols, dq.ptr + t * cols, dd.ptr + t * (cols // 32) * 4,
+                             ds.ptr + t * (cols // 16) * 4, o1.ptr, None)
+        singles.append(o1)
+    nova.dev_sync()
+    got = out4.numpy((4, rows), np.float32)
+    check = slice(None) if rows <= 600 else slice(0, rows, max(rows // 300, 1))
+    for t in range(4):
+        one = singles[t].numpy((rows,), np.float32)
+        assert np.array_equal(got[t].view(np.uint32), one.view(np.uint32)), f"token {t}"
+        ref = oracle.gemv_q4k(w, rows, cols, qs[t:t + 1], d[t:t + 1], s[t:t + 1])
+        scale = abs_terms(oracle, w[check], len(range(rows)[check]), cols, qs[t:t + 1], d[t:t + 1])
+        err = np.abs(got[t][check].astype(np.float64) - ref[check])
+        assert np.all(err <= 2e-6 * scale), f"token {t}: max err/scale {np.max(err / scale):.2e}"

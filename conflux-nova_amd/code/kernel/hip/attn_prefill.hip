@@ -214,18 +214,30 @@ __device__ int lpt_item(const PrefillArgs& a, int r, int n_cg, int n_cols, int c
     return item;
 }
 
-__device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
-
-// direct 16 B per lane global -> LDS load; the wave writes 1 KiB at LDS byte
-// address lds (wave-uniform).
+// The four direct global -> LDS loads of a tile stage, 16 B per lane: load u
+// makes the wave write 1 KiB at LDS byte address lds + 16*THREADS*u
+// (wave-uniform), taken from m0 when the load issues.
 // Issued as inline asm so that the compiler's own vmcnt bookkeeping does not
-// see it: the builtin makes the compiler drain every pending load (including
+// see them: the builtin makes the compiler drain every pending load (including
 // the tiles still meant to be in flight) before each LDS read it cannot prove
 // disjoint.  The pipeline waits for these loads explicitly (tile_barrier);
 // the compiler's waits for its own loads stay correct, as the counter drains
-// in issue order.
-__device__ __forceinline__ void dma16(const void* src, uint32_t lds) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds) : "memory", "m0");
+// in issue order.  m0 is a register the compiler reserves (it cannot be
+// declared clobbered), so the statement saves and restores it.
+__device__ __forceinline__ void dma16x4(const void* s0, const void* s1, const void* s2, const void* s3,
+                                        uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %5\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+        "s_mov_b32 m0, %6\n\tglobal_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %7\n\tglobal_load_lds_dwordx4 %3, off\n\t"
+        "s_mov_b32 m0, %8\n\tglobal_load_lds_dwordx4 %4, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(s0), "v"(s1), "v"(s2), "v"(s3), "s"(lds), "s"(lds + 16u * THREADS), "s"(lds + 32u * THREADS),
+          "s"(lds + 48u * THREADS)
+        : "memory");
 }
 
 // LDS byte address of a __shared__ location
@@ -253,12 +265,6 @@ __device__ __forceinline__ float rows_max(float v) {
     v = fmaxf(__uint_as_float(x[0]), __uint_as_float(x[1]));
     auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
     return fmaxf(__uint_as_float(y[0]), __uint_as_float(y[1]));
-}
-__device__ __forceinline__ float rows_sum(float v) {
-    auto x = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(x[0]) + __uint_as_float(x[1]);
-    auto y = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(y[0]) + __uint_as_float(y[1]);
 }
 
 // 4 halfs of a 16-bit matrix, transposed across each group of 16 lanes
@@ -380,23 +386,22 @@ prefill_kernel(PrefillArgs a) {
         const int64_t b1 = (layer_page0 + __builtin_amdgcn_readfirstlane(pp.p1)) * kPageBytes + kvh * ROWB;
         const uint32_t m0base = __builtin_amdgcn_readfirstlane(lds_addr(&s_kv[kg][BI][0])) + 1024u * wave_s;
         if (TILE * (T + 1) <= key_end) {
-#pragma unroll
-            for (int u = 0; u < LOADS; ++u)
-                dma16((u < 2 ? pk + loff_k : pv + loff_v) + ((u & 1) ? b1 : b0), m0base + 16u * THREADS * u);
+            dma16x4(pk + loff_k + b0, pk + loff_k + b1, pv + loff_v + b0, pv + loff_v + b1, m0base);
         } else {
             // the tile holding the last key: rows past it (never written, may
             // hold NaN bits) load the last key's row instead; their weights are
             // masked to zero
             const int rl = key_end - 1 - TILE * T;           // in [0, TILE)
             const int64_t bl = ((rl >> 4) ? b1 : b0) + (int64_t)(rl & 15) * (KVW * 2);
+            const void* src[LOADS];
 #pragma unroll
             for (int u = 0; u < LOADS; ++u) {
                 const int row = srow + 16 * (u & 1);
                 const char* pool = u < 2 ? pk + 16 * schunk_k : pv + 16 * schunk_v;
                 const int64_t rowoff = (int64_t)srow * (KVW * 2);
-                dma16(TILE * T + row < key_end ? pool + ((u & 1) ? b1 : b0) + rowoff : pool + bl,
-                      m0base + 16u * THREADS * u);
+                src[u] = TILE * T + row < key_end ? pool + ((u & 1) ? b1 : b0) + rowoff : pool + bl;
             }
+            dma16x4(src[0], src[1], src[2], src[3], m0base);
         }
     };
 

@@ -13,11 +13,12 @@
 //  * A workgroup of 4 waves stages the whole activation (codes, scales, sums)
 //    in LDS once and then walks rows (grid-stride), one row per wave at a
 //    time, so the activation is read from L2 once per workgroup, not per row.
-//  * A wave covers 8 super-blocks per step: lane (j, c) = (lane >> 3, lane & 7)
-//    takes the 16 nibble bytes at offset 16c of super-block 8s + j -- 16 weights
-//    of sub-block 2(c>>1) (low nibbles) and 16 of sub-block 2(c>>1)+1 (high).
-//    Rows of up to 4 steps (cols <= 8192: the hidden widths 1536, 3584,
-//    5120) are one wave's, with the step loop unrolled at compile time and
+//  * One token: a wave covers 16 super-blocks per step: lane (j, c) =
+//    (lane >> 2, lane & 3) takes the 32 nibble bytes at offset 32c of
+//    super-block 16s + j -- all 32 weights of sub-block 2c (low nibbles) and
+//    of 2c+1 (high).  (The four-token kernel uses half-width lanes, 8
+//    super-blocks per step.)  Rows of up to 4 steps (cols <= 16384: the
+//    hidden widths 1536, 3584, 5120) are one wave's, with the step loop unrolled at compile time and
 //    all of a row's loads issued before any is consumed; wider rows (the FFN
 //    widths) are shared by the 4 waves of a workgroup, at most 4 steps each,
 //    reduced through LDS in a fixed order.  Grids are sized to what is
@@ -42,6 +43,26 @@ constexpr int kQK = 256;                       // weights per super-block
 constexpr int kBlockBytes = 144;
 constexpr int QT = 256;                        // threads per workgroup
 constexpr int kMaxCols = 32768;                // the activation (and its scales, sums) fits LDS
+// Lane geometry, LPS = lanes per super-block.  LPS = 4 (one token): a lane
+// owns the 32 nibble bytes of one sub-block pair (64 weights: sub-block 2c in
+// the low nibbles, 2c+1 in the high), 16 super-blocks per wave step.  LPS = 8
+// (four tokens): half of that, 8 super-blocks per step.  Measured: the wide
+// lanes take a 7B layer's projections from 50.8 to 48.7 us (fewer, larger
+// steps per row), but make the four-token kernel 11% slower.
+template <int LPS>
+struct Lanes {
+    static_assert(LPS == 4 || LPS == 8, "4 or 8 lanes per super-block");
+    static constexpr int kSbPerStep = 64 / LPS;
+    static constexpr int kNibWords = 32 / LPS;   // nibble dwords per lane
+    static constexpr int grp(int c) { return LPS == 4 ? c : c >> 1; }
+    static constexpr int elo(int c) { return LPS == 4 ? 64 * c : (c >> 1) * 64 + (c & 1) * 16; }
+};
+constexpr int kLps1 = 4;                       // one-token kernels
+constexpr int kLps4 = 8;                       // four-token kernel
+template <int LPS>
+struct Nib {
+    uint32_t w[Lanes<LPS>::kNibWords];
+};
 
 // ---------------------------------------------------------------- quant
 // One 32-element block of quant_kernel, q4k_gemv.cu:9-33: d = amax / 127,
@@ -119,17 +140,34 @@ __device__ __forceinline__ void scale_min(int j, const uint32_t sw[3], uint32_t&
 // high) and the two (d*scale, dmin*min) pairs; sb_dot takes the products with
 // one activation staged in LDS (codes, scales per 32, sums per 16).  The
 // float combination is the reference's: dx * (d*sc*sum(q*c) - dmin*m*sum(c)).
+template <int LPS>
 struct SbW {
-    int lo[4], hi[4];          // nibbles as int8 lanes for v_dot4_i32_i8
-    float al, bl, ah, bh;      // d*sc and dmin*m of the two sub-blocks
+    static constexpr int NW = Lanes<LPS>::kNibWords;
+    int lo[NW], hi[NW];                // nibbles as int8 lanes for v_dot4_i32_i8
+    float al, bl, ah, bh;              // d*sc and dmin*m of the two sub-blocks
 };
 
-__device__ __forceinline__ SbW sb_prep(const u4 hd, const u4 nb16, int grp) {
-    SbW w;
+template <int LPS>
+__device__ __forceinline__ Nib<LPS> load_nib(const uint8_t* blk, int c) {
+    constexpr int NW = Lanes<LPS>::kNibWords;
+    Nib<LPS> n;
+    const uint8_t* p = blk + 16 + 4 * NW * c;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        w.lo[e] = (int)(nb16[e] & 0x0F0F0F0Fu);
-        w.hi[e] = (int)((nb16[e] >> 4) & 0x0F0F0F0Fu);
+    for (int h = 0; h < NW / 4; ++h) {
+        const u4 v = *reinterpret_cast<const u4*>(p + 16 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) n.w[4 * h + e] = v[e];
+    }
+    return n;
+}
+
+template <int LPS>
+__device__ __forceinline__ SbW<LPS> sb_prep(const u4 hd, const Nib<LPS>& nb, int grp) {
+    SbW<LPS> w;
+#pragma unroll
+    for (int e = 0; e < SbW<LPS>::NW; ++e) {
+        w.lo[e] = (int)(nb.w[e] & 0x0F0F0F0Fu);
+        w.hi[e] = (int)((nb.w[e] >> 4) & 0x0F0F0F0Fu);
     }
     const uint32_t sw[3] = {hd[1], hd[2], hd[3]};
     uint32_t scl, mcl, sch, mch;
@@ -145,24 +183,34 @@ __device__ __forceinline__ SbW sb_prep(const u4 hd, const u4 nb16, int grp) {
 }
 
 // k0: the lane's first element (low nibbles) in the row; high nibbles at k0 + 32
-__device__ __forceinline__ float sb_dot(const SbW& w, int k0, const int8_t* s_q, const float* s_d,
+template <int LPS>
+__device__ __forceinline__ float sb_dot(const SbW<LPS>& w, int k0, const int8_t* s_q, const float* s_d,
                                         const int32_t* s_s) {
-    const i4 alo = *reinterpret_cast<const i4*>(s_q + k0);
-    const i4 ahi = *reinterpret_cast<const i4*>(s_q + k0 + 32);
+    constexpr int NW = SbW<LPS>::NW;
     int dlo = 0, dhi = 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        dlo = __builtin_amdgcn_sdot4(w.lo[e], alo[e], dlo, false);
-        dhi = __builtin_amdgcn_sdot4(w.hi[e], ahi[e], dhi, false);
+    for (int h = 0; h < NW / 4; ++h) {
+        const i4 alo = *reinterpret_cast<const i4*>(s_q + k0 + 16 * h);
+        const i4 ahi = *reinterpret_cast<const i4*>(s_q + k0 + 32 + 16 * h);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            dlo = __builtin_amdgcn_sdot4(w.lo[4 * h + e], alo[e], dlo, false);
+            dhi = __builtin_amdgcn_sdot4(w.hi[4 * h + e], ahi[e], dhi, false);
+        }
     }
     const float dxl = s_d[k0 >> 5], dxh = s_d[(k0 + 32) >> 5];
-    const int sml = s_s[k0 >> 4], smh = s_s[(k0 + 32) >> 4];
+    int sml = s_s[k0 >> 4], smh = s_s[(k0 + 32) >> 4];
+    if constexpr (NW == 8) {                   // 32 elements: both 16-sums
+        sml += s_s[(k0 >> 4) + 1];
+        smh += s_s[((k0 + 32) >> 4) + 1];
+    }
     return dxl * (w.al * (float)dlo - w.bl * (float)sml) + dxh * (w.ah * (float)dhi - w.bh * (float)smh);
 }
 
-__device__ __forceinline__ float sb_terms(const u4 hd, const u4 nb16, int sb, int grp, int elo,
+template <int LPS>
+__device__ __forceinline__ float sb_terms(const u4 hd, const Nib<LPS>& nb, int sb, int grp, int elo,
                                           const int8_t* s_q, const float* s_d, const int32_t* s_s) {
-    return sb_dot(sb_prep(hd, nb16, grp), sb * kQK + elo, s_q, s_d, s_s);
+    return sb_dot<LPS>(sb_prep<LPS>(hd, nb, grp), sb * kQK + elo, s_q, s_d, s_s);
 }
 
 // Up to 4 matrices of the same width that read one activation (q/k/v,
@@ -220,6 +268,7 @@ __device__ __forceinline__ void stage_activation(const GemvSet& g, int8_t* s_q, 
 // keeps more bytes in flight per wave but costs occupancy and is slower.)
 template <int STEPS, bool kF32>
 __global__ void __launch_bounds__(QT) gemv_fixed_kernel(GemvSet g) {
+    constexpr int LPS_ = kLps1;
     extern __shared__ __attribute__((aligned(16))) unsigned char s_x[];
     const int cols = g.cols;
     int8_t* s_q = reinterpret_cast<int8_t*>(s_x);
@@ -229,8 +278,9 @@ __global__ void __launch_bounds__(QT) gemv_fixed_kernel(GemvSet g) {
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar row addressing
-    const int j = lane >> 3, c = lane & 7, grp = c >> 1;
-    const int elo = grp * 64 + (c & 1) * 16;
+    using L = Lanes<LPS_>;
+    const int j = lane / LPS_, c = lane % LPS_, grp = L::grp(c);
+    const int elo = L::elo(c);
     const int nsb = cols / kQK;
     const int64_t row_bytes = (int64_t)nsb * kBlockBytes;
     const int64_t rows = kF32 ? g.end[g.n - 1] : g.end[0];   // one matrix on the ActQ8 path
@@ -239,21 +289,22 @@ __global__ void __launch_bounds__(QT) gemv_fixed_kernel(GemvSet g) {
         const int m = kF32 ? mat_of(g, r) : 0;
         const int64_t lr = m ? r - g.end[m - 1] : r;
         const uint8_t* wr = g.w[m] + lr * row_bytes;
-        u4 hdr[STEPS], nib[STEPS];
+        u4 hdr[STEPS];
+        Nib<LPS_> nib[STEPS];
 #pragma unroll
         for (int t = 0; t < STEPS; ++t) {
-            const int sb = 8 * t + j;
+            const int sb = L::kSbPerStep * t + j;
             if (sb < nsb) {
                 const uint8_t* blk = wr + (int64_t)sb * kBlockBytes;
                 hdr[t] = *reinterpret_cast<const u4*>(blk);
-                nib[t] = *reinterpret_cast<const u4*>(blk + 16 + 16 * c);
+                nib[t] = load_nib<LPS_>(blk, c);
             }
         }
         float acc = 0.f;
 #pragma unroll
         for (int t = 0; t < STEPS; ++t) {
-            const int sb = 8 * t + j;
-            if (sb < nsb) acc += sb_terms(hdr[t], nib[t], sb, grp, elo, s_q, s_d, s_s);
+            const int sb = L::kSbPerStep * t + j;
+            if (sb < nsb) acc += sb_terms<LPS_>(hdr[t], nib[t], sb, grp, elo, s_q, s_d, s_s);
         }
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
@@ -267,6 +318,7 @@ __global__ void __launch_bounds__(QT) gemv_fixed_kernel(GemvSet g) {
 // iteration.
 template <int STEPS, int KS, bool kF32>
 __global__ void __launch_bounds__(QT) gemv_split_kernel(GemvSet g) {
+    constexpr int LPS_ = kLps1;
     extern __shared__ __attribute__((aligned(16))) unsigned char s_x[];
     __shared__ float s_part[4];
     const int cols = g.cols;
@@ -279,10 +331,11 @@ __global__ void __launch_bounds__(QT) gemv_split_kernel(GemvSet g) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar row addressing
     const int part = wave % KS;
-    const int j = lane >> 3, c = lane & 7, grp = c >> 1;
-    const int elo = grp * 64 + (c & 1) * 16;
+    using L = Lanes<LPS_>;
+    const int j = lane / LPS_, c = lane % LPS_, grp = L::grp(c);
+    const int elo = L::elo(c);
     const int nsb = cols / kQK;
-    const int sb0 = 8 * STEPS * part + j;
+    const int sb0 = L::kSbPerStep * STEPS * part + j;
     const int64_t row_bytes = (int64_t)nsb * kBlockBytes;
     const int64_t rows = kF32 ? g.end[g.n - 1] : g.end[0];   // one matrix on the ActQ8 path
     const int64_t stride = (int64_t)gridDim.x * RPI;
@@ -294,20 +347,21 @@ __global__ void __launch_bounds__(QT) gemv_split_kernel(GemvSet g) {
         float acc = 0.f;
         if (r < rows) {
             const uint8_t* wr = g.w[m] + lr * row_bytes;
-            u4 hdr[STEPS], nib[STEPS];
+            u4 hdr[STEPS];
+            Nib<LPS_> nib[STEPS];
 #pragma unroll
             for (int t = 0; t < STEPS; ++t) {
-                const int sb = sb0 + 8 * t;
+                const int sb = sb0 + L::kSbPerStep * t;
                 if (sb < nsb) {
                     const uint8_t* blk = wr + (int64_t)sb * kBlockBytes;
                     hdr[t] = *reinterpret_cast<const u4*>(blk);
-                    nib[t] = *reinterpret_cast<const u4*>(blk + 16 + 16 * c);
+                    nib[t] = load_nib<LPS_>(blk, c);
                 }
             }
 #pragma unroll
             for (int t = 0; t < STEPS; ++t) {
-                const int sb = sb0 + 8 * t;
-                if (sb < nsb) acc += sb_terms(hdr[t], nib[t], sb, grp, elo, s_q, s_d, s_s);
+                const int sb = sb0 + L::kSbPerStep * t;
+                if (sb < nsb) acc += sb_terms<LPS_>(hdr[t], nib[t], sb, grp, elo, s_q, s_d, s_s);
             }
         }
 #pragma unroll
@@ -328,9 +382,9 @@ __global__ void __launch_bounds__(QT) gemv_split_kernel(GemvSet g) {
 // Engine::decode_batch uses it for every projection, model.cpp:270-311):
 // each weight load and its scale unpacking serve four activations.  The four
 // activations (4 x 1.375 B per column) sit in LDS, 104 KB at the FFN width,
-// so a workgroup is 16 waves to keep the CU's waves up.  Rows map to waves
-// exactly as in the one-token kernels (STEPS, KS), and every token's
-// arithmetic is theirs: each output equals launch_gemv_q4k's for that token.
+// so a workgroup is 16 waves to keep the CU's waves up.  Lanes are half as
+// wide as in the one-token kernels (8 per super-block), so each token's sum
+// is taken in another order than launch_gemv_q4k's (same terms).
 constexpr int kTok4 = 4;
 constexpr int QT4 = 1024;                      // threads per workgroup
 constexpr int kMaxCols4 = 28672;               // 4 activations within 160 KB of LDS
@@ -339,6 +393,7 @@ template <int STEPS, int KS>
 __global__ void __launch_bounds__(QT4) gemv4_kernel(const uint8_t* __restrict__ w, int64_t rows, int cols,
                                                      const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                      const int32_t* __restrict__ xs, float* __restrict__ out) {
+    constexpr int LPS_ = kLps4;
     extern __shared__ __attribute__((aligned(16))) unsigned char s_x[];
     __shared__ float s_part[QT4 / 64][kTok4];
     int8_t* s_q = reinterpret_cast<int8_t*>(s_x);                                   // [4][cols]
@@ -355,10 +410,11 @@ __global__ void __launch_bounds__(QT4) gemv4_kernel(const uint8_t* __restrict__ 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int part = wave % KS;
-    const int j = lane >> 3, c = lane & 7, grp = c >> 1;
-    const int elo = grp * 64 + (c & 1) * 16;
+    using L = Lanes<LPS_>;
+    const int j = lane / LPS_, c = lane % LPS_, grp = L::grp(c);
+    const int elo = L::elo(c);
     const int nsb = cols / kQK;
-    const int sb0 = 8 * STEPS * part + j;
+    const int sb0 = L::kSbPerStep * STEPS * part + j;
     const int64_t row_bytes = (int64_t)nsb * kBlockBytes;
     const int64_t stride = (int64_t)gridDim.x * RPI;
 
@@ -367,24 +423,25 @@ __global__ void __launch_bounds__(QT4) gemv4_kernel(const uint8_t* __restrict__ 
         float acc[kTok4] = {0.f, 0.f, 0.f, 0.f};
         if (r < rows) {
             const uint8_t* wr = w + r * row_bytes;
-            u4 hdr[STEPS], nib[STEPS];
+            u4 hdr[STEPS];
+            Nib<LPS_> nib[STEPS];
 #pragma unroll
             for (int t = 0; t < STEPS; ++t) {
-                const int sb = sb0 + 8 * t;
+                const int sb = sb0 + L::kSbPerStep * t;
                 if (sb < nsb) {
                     const uint8_t* blk = wr + (int64_t)sb * kBlockBytes;
                     hdr[t] = *reinterpret_cast<const u4*>(blk);
-                    nib[t] = *reinterpret_cast<const u4*>(blk + 16 + 16 * c);
+                    nib[t] = load_nib<LPS_>(blk, c);
                 }
             }
 #pragma unroll
             for (int t = 0; t < STEPS; ++t) {
-                const int sb = sb0 + 8 * t;
+                const int sb = sb0 + L::kSbPerStep * t;
                 if (sb < nsb) {
-                    const SbW wv = sb_prep(hdr[t], nib[t], grp);
+                    const SbW<LPS_> wv = sb_prep<LPS_>(hdr[t], nib[t], grp);
 #pragma unroll
                     for (int k = 0; k < kTok4; ++k)
-                        acc[k] += sb_dot(wv, sb * kQK + elo, s_q + k * cols, s_d + k * (cols / 32),
+                        acc[k] += sb_dot<LPS_>(wv, sb * kQK + elo, s_q + k * cols, s_d + k * (cols / 32),
                                          s_s + k * (cols / 16));
                 }
             }
@@ -459,7 +516,8 @@ template <bool kF32>
 void launch_set(const GemvSet& g, hipStream_t st) {
     const int cols = g.cols;
     const size_t lds = (size_t)cols + 4 * (size_t)(cols / 32) + 4 * (size_t)(cols / 16);
-    switch ((cols / kQK + 7) / 8) {            // steps of 8 super-blocks
+    constexpr int SPS = Lanes<kLps1>::kSbPerStep;
+    switch ((cols / kQK + SPS - 1) / SPS) {    // steps of SPS super-blocks
         case 1: launch_fixed<1, kF32>(g, lds, st); break;
         case 2: launch_fixed<2, kF32>(g, lds, st); break;
         case 3: launch_fixed<3, kF32>(g, lds, st); break;
@@ -513,7 +571,8 @@ void launch_gemv4_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_
     if (rows == 0) return;
     const size_t lds = kTok4 * ((size_t)cols + 4 * (size_t)(cols / 32) + 4 * (size_t)(cols / 16));
     const hipStream_t st = reinterpret_cast<hipStream_t>(s);
-    switch ((cols / kQK + 7) / 8) {            // the one-token kernels' row shapes
+    constexpr int SPS = Lanes<kLps4>::kSbPerStep;
+    switch ((cols / kQK + SPS - 1) / SPS) {    // steps of SPS super-blocks: the row shapes
         case 1: launch_gemv4_shape<1, 1>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
         case 2: launch_gemv4_shape<2, 1>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;
         case 3: launch_gemv4_shape<3, 1>(blocks, rows, cols, xq, xd, xs, out, lds, st); break;

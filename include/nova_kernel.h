@@ -208,7 +208,8 @@ void launch_gemv_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_t
  * Engine::decode_batch uses for every projection (model.cpp:270-311).  The
  * four ActQ8 activations are stacked: xq [4][cols], xd [4][cols/32],
  * xs [4][cols/16]; out [4][rows].  Each weight is read once for the four
- * tokens, and out[t] is bit-identical to launch_gemv_q4k on token t.
+ * tokens; out[t] equals launch_gemv_q4k on token t up to fp32 summation
+ * order (the same terms, summed in another order).
  * cols % 256 == 0, cols <= 28672. */
 void launch_gemv4_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_t* xq, const float* xd,
                       const int32_t* xs, float* out, nova_stream_t s);

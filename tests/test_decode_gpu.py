@@ -234,3 +234,39 @@ def test_decode_batch_rope_fused(model, oracle):
                                              int(n_keys[i]))
             assert np.abs(plain - ref).max() > 1e-3, "rotation had no effect"
     print(f"  worst max|gpu-oracle|={worst:.3e}")
+
+
+def _decode_f64(q, hk, hv, table, n_keys, group):
+    """Textbook softmax attention in float64 for one session (the reference the
+    C oracle is pinned to), vectorised for very long contexts."""
+    pos = np.arange(n_keys)
+    k = hk[table[pos >> 4], pos & 15].view(np.float16).astype(np.float64)   # [n_keys][NKV][HD]
+    v = hv[table[pos >> 4], pos & 15].view(np.float16).astype(np.float64)
+    qh = q.astype(np.float64).reshape(k.shape[1], group, q.shape[-1])          # [NKV][G][HD]
+    s = np.einsum("ngd,knd->ngk", qh, k) / np.sqrt(q.shape[-1])
+    s -= s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.einsum("ngk,knd->ngd", p, v).reshape(q.shape)
+
+
+def test_decode_long_ranges():
+    """Split workgroups that own more than 64 pages reload their block-table
+    slice while they stream: the single-session entry point from ~32K keys
+    (at most 31 splits), the batched one once the batch exceeds 256 x 64
+    pages (share > 64)."""
+    import nova_amd
+    nova = nova_amd.load("qwen25_1p5b")
+    n_keys = np.array([140000, 130001], np.int32)
+    pages = (n_keys + 15) // 16
+    print(f"[case] decode long ranges n_keys={n_keys.tolist()} pages={int(pages.sum())}", flush=True)
+    assert int(pages.sum()) > 256 * 64
+    fx = PagedFixture(nova, nb=2 * int(pages.max()) + 4, layer=LAYER, seed=41)
+    tables = fx.tables(2, int(pages.max()))
+    q = fx.rng.standard_normal((2, nova.nh, nova.hd)).astype(np.float32)
+    ref = [_decode_f64(q[i], fx.hk, fx.hv, tables[i], int(n_keys[i]), nova.group) for i in range(2)]
+    got = _batch(nova, fx, q, tables, n_keys)
+    for i in range(2):
+        assert_close(got[i], ref[i], what=f"batched session {i}")
+    one = _decode_single(nova, fx, np.ascontiguousarray(q[1]), np.ascontiguousarray(tables[1]), 40000)
+    assert_close(one, _decode_f64(q[1], fx.hk, fx.hv, tables[1], 40000, nova.group), what="single 40000 keys")

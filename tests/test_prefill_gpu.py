@@ -184,3 +184,49 @@ def test_prefill_batch_wide_ranked(nova7, oracle):
                                         n_q, int(n_past[i]))
         err = assert_close(got[i], ref, what=f"session {i}")
         print(f"  session {i} max|gpu-oracle|={err:.3e}")
+
+
+def _causal_f64(q, hk, hv, table, n_q, n_past, group):
+    """Textbook causal softmax attention in float64 over the paged pool (the
+    reference the C oracle is itself pinned to), vectorised: the C oracle
+    replays the reference's per-warp arithmetic and needs ~50 s at 40K keys."""
+    n_keys = n_past + n_q
+    pos = np.arange(n_keys)
+    k = hk[table[pos >> 4], pos & 15].view(np.float16).astype(np.float64)   # [n_keys][NKV][HD]
+    v = hv[table[pos >> 4], pos & 15].view(np.float16).astype(np.float64)
+    kh = np.repeat(k, group, axis=1)                                          # [n_keys][NH][HD]
+    vh = np.repeat(v, group, axis=1)
+    s = np.einsum("qhd,khd->qhk", q.astype(np.float64), kh) / np.sqrt(q.shape[-1])
+    mask = pos[None, :] > (n_past + np.arange(n_q))[:, None]                  # [n_q][n_keys]
+    s = np.where(mask[:, None, :], -np.inf, s)
+    s -= s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return np.einsum("qhk,khd->qhd", p, vh)
+
+
+@pytest.mark.parametrize("n_q,n_past", [(24, 40000), (40, 32760)])
+def test_prefill_beyond_table_window(n_q, n_past):
+    """Prefixes past 2048 pages (32K tokens): the workgroups' LDS window of the
+    block table is reloaded while the tiles stream, single call and batched."""
+    import nova_amd
+    nova = nova_amd.load("qwen25_1p5b")
+    print(f"[case] prefill long prefix n_q={n_q} n_past={n_past}", flush=True)
+    pages = (n_past + n_q + 15) // 16
+    fx = PagedFixture(nova, nb=2 * pages + 4, layer=LAYER, seed=n_past)
+    tables = fx.tables(2, pages)
+    q = fx.rng.standard_normal((2, n_q, nova.nh, nova.hd)).astype(np.float32)
+    got1 = _prefill(nova, fx, np.ascontiguousarray(q[0]), tables[0], n_q, n_past)
+    ref0 = _causal_f64(q[0], fx.hk, fx.hv, tables[0], n_q, n_past, nova.group)
+    err = assert_close(got1, ref0, what=f"single n_past={n_past}")
+    n_pasts = np.array([n_past, 300], np.int32)
+    dq, dt, dn = nova.upload(q), nova.upload(tables), nova.upload(n_pasts)
+    do = nova.upload(np.full(q.shape, np.nan, np.float32))
+    nova.launch_attn_prefill_paged_batch(dq.ptr, fx.k.ptr, fx.v.ptr, dt.ptr, pages, dn.ptr, 2, n_q, LAYER, fx.nb,
+                                         do.ptr, None)
+    nova.dev_sync()
+    got = do.numpy(q.shape, np.float32)
+    assert_close(got[0], ref0, what="batched long session")
+    ref1 = _causal_f64(q[1], fx.hk, fx.hv, tables[1], n_q, 300, nova.group)
+    assert_close(got[1], ref1, what="batched short session")
+    print(f"  max|gpu-f64|={err:.3e}")

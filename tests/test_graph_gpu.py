@@ -1,0 +1,174 @@
+"""HIP-graph replays of the hot path equal its eager run.
+
+The benchmark replays whole decode steps, prefill layers and GEMV layers from
+HIP graphs.  A captured graph must hold no memset node (only fill kernels), so
+replays after the first see the same state; each test captures a step, replays
+it several times with unrelated eager work and synchronisations in between,
+and requires every replay to reproduce the eager outputs bit for bit (the
+appends rewrite the same slots with the same bits, so a step is idempotent).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from helpers import PagedFixture, f16
+
+pytestmark = pytest.mark.gpu
+LAYERS = (0, 3, 7)
+
+
+def _replays(nova, s, run, read, n=4):
+    """eager run, then n graph replays of the same launches; returns outputs"""
+    run()
+    nova.dev_stream_sync(s)
+    eager = read()
+    nova.dev_graph_begin(s)
+    run()
+    g = nova.dev_graph_end(s)
+    junk = nova.alloc(1 << 20)
+    outs = []
+    try:
+        for r in range(n):
+            nova.dev_zero(junk.ptr, junk.nbytes, s)          # unrelated eager work between replays
+            nova.dev_stream_sync(s)
+            nova.dev_graph_launch(g, s)
+            nova.dev_stream_sync(s)
+            outs.append(read())
+    finally:
+        nova.dev_graph_destroy(g)
+    return eager, outs
+
+
+def test_decode_step_graph(nova7):
+    """plan + fused-append decode of three layers for 6 ragged sessions"""
+    nova = nova7
+    print("[case] graph decode step", flush=True)
+    n_keys = np.array([700, 1, 33, 2048, 16, 300], np.int32)
+    n = len(n_keys)
+    pages = int((n_keys.max() + 15) // 16)
+    fx = PagedFixture(nova, nb=n * pages + 3, layer=LAYERS[0], seed=12)
+    tables = fx.tables(n, pages)
+    rng = np.random.default_rng(5)
+    q = nova.upload(rng.standard_normal((len(LAYERS), n, nova.nh, nova.hd)).astype(np.float32))
+    kn = nova.upload(f16(rng, (len(LAYERS), n, nova.nkv, nova.hd)))
+    vn = nova.upload(f16(rng, (len(LAYERS), n, nova.nkv, nova.hd)))
+    o = nova.upload(np.full((len(LAYERS), n, nova.nh, nova.hd), np.nan, np.float32))
+    ws = nova.alloc(nova.attn_decode_batch_workspace_bytes(n))
+    dt, dn = nova.upload(tables), nova.upload(n_keys)
+    s = nova.dev_stream_create()
+    qs, kvs = n * nova.nh * nova.hd, n * nova.kvw
+
+    def run():
+        nova.launch_attn_decode_plan(dt.ptr, pages, dn.ptr, n, ws.ptr, s)
+        for i, layer in enumerate(LAYERS):
+            nova.launch_attn_decode_paged_planned(q.ptr + i * qs * 4, fx.k.ptr, fx.v.ptr, dt.ptr, pages, n, layer,
+                                                  fx.nb, kn.ptr + i * kvs * 2, vn.ptr + i * kvs * 2,
+                                                  o.ptr + i * qs * 4, ws.ptr, s)
+
+    eager, outs = _replays(nova, s, run, lambda: o.numpy((len(LAYERS), n, nova.nh, nova.hd), np.float32))
+    assert np.all(np.isfinite(eager))
+    for r, got in enumerate(outs):
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"
+
+
+def test_decode_rope_step_graph(nova7):
+    """the fused RoPE + append + decode step"""
+    nova = nova7
+    print("[case] graph decode rope step", flush=True)
+    n_keys = np.array([90, 1, 4000, 17], np.int32)
+    n = len(n_keys)
+    pages = int((n_keys.max() + 15) // 16)
+    fx = PagedFixture(nova, nb=n * pages + 3, layer=LAYERS[0], seed=13)
+    tables = fx.tables(n, pages)
+    half = nova.hd // 2
+    cs, sn = nova.alloc(4096 * half * 4), nova.alloc(4096 * half * 4)
+    nova.launch_rope_table(cs.ptr, sn.ptr, None)
+    rng = np.random.default_rng(6)
+    q = nova.upload(rng.standard_normal((len(LAYERS), n, nova.nh, nova.hd)).astype(np.float32))
+    k = nova.upload(rng.standard_normal((len(LAYERS), n, nova.nkv, nova.hd)).astype(np.float32))
+    v = nova.upload(rng.standard_normal((len(LAYERS), n, nova.nkv, nova.hd)).astype(np.float32))
+    o = nova.alloc(len(LAYERS) * n * nova.nh * nova.hd * 4)
+    ws = nova.alloc(nova.attn_decode_batch_workspace_bytes(n))
+    dt, dn = nova.upload(tables), nova.upload(n_keys)
+    s = nova.dev_stream_create()
+    qs, kvs = n * nova.nh * nova.hd, n * nova.kvw
+    nova.dev_sync()
+
+    def run():
+        nova.launch_attn_decode_plan(dt.ptr, pages, dn.ptr, n, ws.ptr, s)
+        for i, layer in enumerate(LAYERS):
+            nova.launch_attn_decode_paged_rope_planned(q.ptr + i * qs * 4, k.ptr + i * kvs * 4, v.ptr + i * kvs * 4,
+                                                       cs.ptr, sn.ptr, fx.k.ptr, fx.v.ptr, dt.ptr, pages, n, layer,
+                                                       fx.nb, o.ptr + i * qs * 4, ws.ptr, s)
+
+    eager, outs = _replays(nova, s, run, lambda: o.numpy((len(LAYERS), n, nova.nh, nova.hd), np.float32))
+    assert np.all(np.isfinite(eager))
+    for r, got in enumerate(outs):
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"
+
+
+def test_prefill_layer_graph(nova7):
+    """batched append + causal prefill, 4 sessions"""
+    nova = nova7
+    print("[case] graph prefill", flush=True)
+    n_past = np.array([0, 300, 1000, 47], np.int32)
+    n, n_q = len(n_past), 96
+    pages = int((n_past.max() + n_q + 15) // 16)
+    fx = PagedFixture(nova, nb=n * pages + 3, layer=LAYERS[1], seed=14)
+    tables = fx.tables(n, pages)
+    rng = np.random.default_rng(7)
+    q = nova.upload(rng.standard_normal((n, n_q, nova.nh, nova.hd)).astype(np.float32))
+    kc = nova.upload(f16(rng, (n, n_q, nova.nkv, nova.hd)))
+    vc = nova.upload(f16(rng, (n, n_q, nova.nkv, nova.hd)))
+    o = nova.alloc(n * n_q * nova.nh * nova.hd * 4)
+    dt, dp = nova.upload(tables), nova.upload(n_past)
+    s = nova.dev_stream_create()
+
+    def run():
+        nova.launch_kv_store_paged_batch(fx.k.ptr, fx.v.ptr, dt.ptr, pages, dp.ptr, n, LAYERS[1], fx.nb, n_q,
+                                         kc.ptr, vc.ptr, s)
+        nova.launch_attn_prefill_paged_batch(q.ptr, fx.k.ptr, fx.v.ptr, dt.ptr, pages, dp.ptr, n, n_q, LAYERS[1],
+                                             fx.nb, o.ptr, s)
+
+    eager, outs = _replays(nova, s, run, lambda: o.numpy((n, n_q, nova.nh, nova.hd), np.float32))
+    assert np.all(np.isfinite(eager))
+    for r, got in enumerate(outs):
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"
+
+
+def test_gemv_fused_graph(nova7):
+    """quantise-in-launch GEMV over three matrices, and the four-token GEMV"""
+    nova = nova7
+    print("[case] graph gemv", flush=True)
+    rng = np.random.default_rng(8)
+    cols, rows = 3584, (512, 64, 300)
+    ws = []
+    for r in rows:
+        b = rng.integers(0, 256, (r, cols // 256, 144), dtype=np.uint8)
+        b[..., 0:2] = rng.uniform(2e-4, 4e-3, (r, cols // 256, 1)).astype(np.float16).view(np.uint8)
+        b[..., 2:4] = rng.uniform(1e-4, 2e-3, (r, cols // 256, 1)).astype(np.float16).view(np.uint8)
+        ws.append(nova.upload(b))
+    x = nova.upload(rng.standard_normal(cols).astype(np.float32))
+    x4 = nova.upload(rng.standard_normal((4, cols)).astype(np.float32))
+    outs = [nova.alloc(r * 4) for r in rows]
+    out4 = nova.alloc(4 * rows[0] * 4)
+    qs, dd, sm = nova.alloc(4 * cols), nova.alloc(4 * cols // 8), nova.alloc(4 * cols // 4)
+    s = nova.dev_stream_create()
+    bl = (C.c_void_p * 3)(*[w.ptr for w in ws])
+    rw = (C.c_int64 * 3)(*rows)
+    ou = (C.c_void_p * 3)(*[o.ptr for o in outs])
+
+    def run():
+        nova.launch_gemv_q4k_f32(bl, rw, ou, 3, cols, x.ptr, s)
+        nova.launch_quant_q8(qs.ptr, dd.ptr, sm.ptr, x4.ptr, 4, cols, s)
+        nova.launch_gemv4_q4k(ws[0].ptr, rows[0], cols, qs.ptr, dd.ptr, sm.ptr, out4.ptr, s)
+
+    def read():
+        return np.concatenate([o.numpy((r,), np.float32) for o, r in zip(outs, rows)] +
+                              [out4.numpy((4 * rows[0],), np.float32)])
+
+    eager, reps = _replays(nova, s, run, read)
+    assert np.all(np.isfinite(eager))
+    for r, got in enumerate(reps):
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"

@@ -282,7 +282,6 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
     bytes_step = wl.bytes_per_step()
     gbs = bytes_step / (ms * 1e-3) / 1e9
     k_ms = wl.kernel_ms()
-    rope = wl.rope_compare(args.steps, args.warmup) if model == "qwen25_7b" else None
     bytes_launch = bytes_step / wl.layers
     achieved = bytes_launch / (k_ms * 1e-3) / 1e9
     traffic = load_traffic(workload_name)
@@ -291,17 +290,23 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
             "kernel": "decode_split_kernel + decode_combine_kernel (one launch_attn_decode_paged_planned call)",
             "kernel_us": round(k_ms * 1e3, 2), "bytes_per_launch": bytes_launch}
     cpu = None
+    parity = None
     if not args.no_cpu:
         th = cpu_threads(args)
         secs, out = wl.cpu_sample(0, th)
         # parity at full size on layer 0 (GPU output of the last replay)
         got = nova.download(wl.o, (wl.n, nova.nh, nova.hd), np.float32)
         err = float(np.abs(got - out).max())
+        parity = {"layer0_max_abs_err": err, "ok": err <= 2e-3}
+        if not parity["ok"]:
+            print(f"bench: PARITY FAILURE on layer 0: max|gpu-cpu| = {err:.3e}", file=sys.stderr, flush=True)
         cpu_gbs = (bytes_step / wl.layers) / secs / 1e9
         cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": th, "kind": "port",
                "sample": f"1 of {wl.layers} layers ({cpu_scale_note}); C oracle or_attn_decode_batch, "
                          f"{secs:.2f} s; max|gpu-cpu| on that layer {err:.2e}",
                "us_per_step_equiv": round(secs * wl.layers * 1e6, 1)}
+    # after the parity leg above: it rewrites the outputs and the appended slots
+    rope = wl.rope_compare(args.steps, args.warmup) if model == "qwen25_7b" else None
     line = {
         "metric": metric_cfg["metric"], "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
@@ -310,6 +315,8 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
         "data": "synthetic (seeded N(0,1) K/V, Q; seeded ragged contexts and page shuffle)",
         "config": metric_cfg["config"], "roofline": roof, "cpu_baseline": cpu,
     }
+    if parity:
+        line["parity"] = parity
     if rope:
         line["rope_in_step"] = dict(rope, note="the same step with RoPE of q and the new k in front of each layer: "
                                                "launch_rope_kv_store_paged_batch + planned decode, against "
@@ -716,7 +723,7 @@ def run_rope(args):
                                "and append k, v as fp16 through the block tables, one launch",
                    "n_past": n_past.tolist(), "chunk": 512},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic("rope"),
                      "kernel": "rope_kernel<true> (launch_rope_kv_store_paged_batch)",
                      "kernel_us": round(ms * 1e3, 2), "bytes_per_launch": nbytes},
         "decode_step_us": round(dec_ms * 1e3, 2),

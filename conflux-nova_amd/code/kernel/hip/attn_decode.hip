@@ -8,8 +8,9 @@
 //
 //  * Work split (session-aligned, balanced).  With T pages in the batch and Gw
 //    target workgroups, session i (P_i pages) gets k_i = ceil(P_i / ceil(T/Gw))
-//    workgroups (the share is at least 8 pages), each owning a contiguous page
-//    range of that session.  Every workgroup does at most that share whatever
+//    workgroups (the share is at least 8 pages, and raised until the
+//    workgroups fit in Gw), each owning a contiguous page range of that
+//    session.  Every workgroup does at most that share whatever
 //    the context lengths, so
 //    a ragged batch fills all CUs evenly, and a workgroup never straddles two
 //    sessions.  Each workgroup writes one partial (m, l, acc[HD]) per head.
@@ -144,6 +145,32 @@ __device__ __forceinline__ int nkeys_of(const DecodeArgs& a, int i) {
     return a.n_keys ? a.n_keys[i] : a.n_keys_scalar;
 }
 
+// Pages per workgroup for the batch: the even share, raised until the
+// sessions' workgroups (sum of ceil(P_i / share)) fit in gw, i.e. in one
+// round of one workgroup per CU (a second round would start after the first
+// has streamed its pages).  Bounded: with more sessions than gw no share fits
+// and the loop gives up.  Wave-uniform; one wave's lanes take 64 sessions at
+// a time.
+__device__ int plan_share(const DecodeArgs& a, int T) {
+    const int lane = threadIdx.x & 63;
+    int target = share_of(T, a.gw);
+    for (int it = 0; it < 64; ++it) {
+        int sumk = 0;
+        for (int base = 0; base < a.n_sess; base += 64) {
+            const int i = base + lane;
+            const int nk = i < a.n_sess ? nkeys_of(a, i) : 0;
+            const int pg = nk > 0 ? (nk + kKvBlock - 1) >> kKvBlockShift : 0;
+            int k = (pg + target - 1) / target;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+            sumk += k;
+        }
+        if (sumk <= a.gw) break;
+        ++target;
+    }
+    return target;
+}
+
 // Find the session that owns workgroup slot w (find_slot) or the partition
 // entry of session `want` (want >= 0).
 __device__ Part partition(const DecodeArgs& a, int w, int want) {
@@ -159,7 +186,7 @@ __device__ Part partition(const DecodeArgs& a, int w, int want) {
     }
     Part r{-1, 0, 0, 0, 0};
     if (T == 0) return r;
-    const int target = share_of(T, a.gw);
+    const int target = plan_share(a, T);
     int carry = 0;
     for (int base = 0; base < a.n_sess; base += 64) {
         const int i = base + lane;
@@ -629,7 +656,7 @@ decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
             for (int o = 1; o < 64; o <<= 1) pg += __shfl_xor(pg, o, 64);
             T += pg;
         }
-        const int target = share_of(T, a.gw);
+        const int target = plan_share(a, T);
         int carry = 0;
         for (int base = 0; base < a.n_sess; base += 64) {
             const int ii = base + lane;

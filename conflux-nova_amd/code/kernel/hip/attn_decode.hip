@@ -696,17 +696,17 @@ decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
     }
 }
 
+// Split workgroups of the batched path: one per CU (an 8-wave workgroup fills
+// the CU's share of waves at this kernel's register count; measured: 2 or 3
+// per CU are slower, 0.97 -> 1.20 -> 1.43 ms per config-2 step).
 int batch_workgroups() {
     static int gw = 0;
     static std::once_flag once;
     std::call_once(once, [] {
-        int per_cu = 1;
-        if (const char* e = std::getenv("NOVA_DECODE_WG_PER_CU")) per_cu = std::atoi(e);
-        if (per_cu < 1) per_cu = 1;
         int dev = 0, cus = 0;
         NOVA_HIP(hipGetDevice(&dev));
         NOVA_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-        gw = cus * per_cu;
+        gw = cus;
     });
     return gw;
 }

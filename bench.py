@@ -175,6 +175,39 @@ class DecodeWorkload:
                 cnt += 1
         return total / cnt
 
+    def per_session_ms(self, steps, warmup):
+        """The reference's call pattern for the same step (Engine::decode_batch,
+        src/model.cpp:282-289): per layer and session one launch_kv_store_paged
+        of the new token and one launch_attn_decode_paged, 2N launches per
+        layer, replayed from a HIP graph; ms per step."""
+        nv, s, L, n = self.nova, self.s, self.layers, self.n
+        scratch = nv.alloc(nv.nh * 32 * (nv.hd + 2) * 4)
+        tab = [self.tables.ptr + i * self.max_pages * 4 for i in range(n)]
+        qs, kvs = n * nv.nh * nv.hd, n * nv.kvw
+
+        def step():
+            for l in range(L):
+                for i in range(n):
+                    nv.launch_kv_store_paged(self.k.ptr, self.v.ptr, tab[i], l, self.nb, 1, int(self.ctx[i]),
+                                             self.knew.ptr + (l * kvs + i * nv.kvw) * 2,
+                                             self.vnew.ptr + (l * kvs + i * nv.kvw) * 2, s)
+                    nv.launch_attn_decode_paged(self.q.ptr + (l * qs + i * nv.nh * nv.hd) * 4, self.k.ptr, self.v.ptr,
+                                                tab[i], l, self.nb, int(self.n_keys[i]),
+                                                self.o.ptr + (l * qs + i * nv.nh * nv.hd) * 4, scratch.ptr, s)
+
+        nv.dev_graph_begin(s)
+        step()
+        g = nv.dev_graph_end(s)
+        for _ in range(warmup):
+            nv.dev_graph_launch(g, s)
+        t = Timer(nv, s)
+        t.start()
+        for _ in range(steps):
+            nv.dev_graph_launch(g, s)
+        ms = t.stop() / steps
+        nv.dev_graph_destroy(g)
+        return ms
+
     def rope_compare(self, steps, warmup):
         """The decode step with RoPE in front of it (a real model's step): the
         separate launch_rope_kv_store_paged_batch + planned decode per layer,
@@ -305,7 +338,8 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
                "sample": f"1 of {wl.layers} layers ({cpu_scale_note}); C oracle or_attn_decode_batch, "
                          f"{secs:.2f} s; max|gpu-cpu| on that layer {err:.2e}",
                "us_per_step_equiv": round(secs * wl.layers * 1e6, 1)}
-    # after the parity leg above: it rewrites the outputs and the appended slots
+    # after the parity leg above: they rewrite the outputs and the appended slots
+    per_session = wl.per_session_ms(args.steps, args.warmup)
     rope = wl.rope_compare(args.steps, args.warmup) if model == "qwen25_7b" else None
     line = {
         "metric": metric_cfg["metric"], "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
@@ -317,6 +351,10 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
     }
     if parity:
         line["parity"] = parity
+    line["per_session_launches"] = {
+        "ms_per_step": round(per_session, 4), "GBs": round(bytes_step / (per_session * 1e-3) / 1e9, 1),
+        "what": "the same step as the reference calls it: per layer and session launch_kv_store_paged + "
+                "launch_attn_decode_paged (2N launches per layer), from a HIP graph"}
     if rope:
         line["rope_in_step"] = dict(rope, note="the same step with RoPE of q and the new k in front of each layer: "
                                                "launch_rope_kv_store_paged_batch + planned decode, against "

@@ -185,7 +185,7 @@ __device__ __forceinline__ SbW<LPS> sb_prep(const u4 hd, const Nib<LPS>& nb, int
 // k0: the lane's first element (low nibbles) in the row; high nibbles at k0 + 32
 template <int LPS>
 __device__ __forceinline__ float sb_dot(const SbW<LPS>& w, int k0, const int8_t* s_q, const float* s_d,
-                                        const int32_t* s_s) {
+                                        const float* s_s) {
     constexpr int NW = SbW<LPS>::NW;
     int dlo = 0, dhi = 0;
 #pragma unroll
@@ -199,17 +199,17 @@ __device__ __forceinline__ float sb_dot(const SbW<LPS>& w, int k0, const int8_t*
         }
     }
     const float dxl = s_d[k0 >> 5], dxh = s_d[(k0 + 32) >> 5];
-    int sml = s_s[k0 >> 4], smh = s_s[(k0 + 32) >> 4];
+    float sml = s_s[k0 >> 4], smh = s_s[(k0 + 32) >> 4];
     if constexpr (NW == 8) {                   // 32 elements: both 16-sums
         sml += s_s[(k0 >> 4) + 1];
         smh += s_s[((k0 + 32) >> 4) + 1];
     }
-    return dxl * (w.al * (float)dlo - w.bl * (float)sml) + dxh * (w.ah * (float)dhi - w.bh * (float)smh);
+    return dxl * (w.al * (float)dlo - w.bl * sml) + dxh * (w.ah * (float)dhi - w.bh * smh);
 }
 
 template <int LPS>
 __device__ __forceinline__ float sb_terms(const u4 hd, const Nib<LPS>& nb, int sb, int grp, int elo,
-                                          const int8_t* s_q, const float* s_d, const int32_t* s_s) {
+                                          const int8_t* s_q, const float* s_d, const float* s_s) {
     return sb_dot<LPS>(sb_prep<LPS>(hd, nb, grp), sb * kQK + elo, s_q, s_d, s_s);
 }
 
@@ -236,9 +236,10 @@ __device__ __forceinline__ int mat_of(const GemvSet& g, int64_t r) {
 }
 
 // The activation (codes, scales per 32, sums per 16) into LDS, once per
-// workgroup; from ActQ8 as given, or quantised here from fp32.
+// workgroup; from ActQ8 as given, or quantised here from fp32.  The sums are
+// kept as floats (exact: |sum| <= 16 * 127), so no dot product converts them.
 template <bool kF32>
-__device__ __forceinline__ void stage_activation(const GemvSet& g, int8_t* s_q, float* s_d, int32_t* s_s) {
+__device__ __forceinline__ void stage_activation(const GemvSet& g, int8_t* s_q, float* s_d, float* s_s) {
     const int cols = g.cols;
     if constexpr (kF32) {
         for (int b = threadIdx.x; b < cols / 32; b += QT) {
@@ -249,14 +250,14 @@ __device__ __forceinline__ void stage_activation(const GemvSet& g, int8_t* s_q, 
             *reinterpret_cast<u4*>(s_q + 32 * b) = lo;
             *reinterpret_cast<u4*>(s_q + 32 * b + 16) = hi;
             s_d[b] = scale;
-            s_s[2 * b] = s0;
-            s_s[2 * b + 1] = s1;
+            s_s[2 * b] = (float)s0;
+            s_s[2 * b + 1] = (float)s1;
         }
     } else {
         for (int i = threadIdx.x; i < cols / 16; i += QT)
             *reinterpret_cast<u4*>(s_q + 16 * i) = *reinterpret_cast<const u4*>(g.xq + 16 * i);
         for (int i = threadIdx.x; i < cols / 32; i += QT) s_d[i] = g.xd[i];
-        for (int i = threadIdx.x; i < cols / 16; i += QT) s_s[i] = g.xs[i];
+        for (int i = threadIdx.x; i < cols / 16; i += QT) s_s[i] = (float)g.xs[i];
     }
     __syncthreads();
 }
@@ -273,7 +274,7 @@ __global__ void __launch_bounds__(QT) gemv_fixed_kernel(GemvSet g) {
     const int cols = g.cols;
     int8_t* s_q = reinterpret_cast<int8_t*>(s_x);
     float* s_d = reinterpret_cast<float*>(s_x + cols);
-    int32_t* s_s = reinterpret_cast<int32_t*>(s_x + cols + 4 * (cols / 32));
+    float* s_s = reinterpret_cast<float*>(s_x + cols + 4 * (cols / 32));   // 16-sums as exact floats
     stage_activation<kF32>(g, s_q, s_d, s_s);
 
     const int lane = threadIdx.x & 63;
@@ -324,7 +325,7 @@ __global__ void __launch_bounds__(QT) gemv_split_kernel(GemvSet g) {
     const int cols = g.cols;
     int8_t* s_q = reinterpret_cast<int8_t*>(s_x);
     float* s_d = reinterpret_cast<float*>(s_x + cols);
-    int32_t* s_s = reinterpret_cast<int32_t*>(s_x + cols + 4 * (cols / 32));
+    float* s_s = reinterpret_cast<float*>(s_x + cols + 4 * (cols / 32));   // 16-sums as exact floats
     stage_activation<kF32>(g, s_q, s_d, s_s);
 
     constexpr int RPI = 4 / KS;
@@ -398,11 +399,11 @@ __global__ void __launch_bounds__(QT4) gemv4_kernel(const uint8_t* __restrict__ 
     __shared__ float s_part[QT4 / 64][kTok4];
     int8_t* s_q = reinterpret_cast<int8_t*>(s_x);                                   // [4][cols]
     float* s_d = reinterpret_cast<float*>(s_x + kTok4 * cols);                       // [4][cols/32]
-    int32_t* s_s = reinterpret_cast<int32_t*>(s_x + kTok4 * cols + 4 * kTok4 * (cols / 32));   // [4][cols/16]
+    float* s_s = reinterpret_cast<float*>(s_x + kTok4 * cols + 4 * kTok4 * (cols / 32));   // [4][cols/16]
     for (int i = threadIdx.x; i < kTok4 * cols / 16; i += QT4)
         *reinterpret_cast<u4*>(s_q + 16 * i) = *reinterpret_cast<const u4*>(xq + 16 * i);
     for (int i = threadIdx.x; i < kTok4 * cols / 32; i += QT4) s_d[i] = xd[i];
-    for (int i = threadIdx.x; i < kTok4 * cols / 16; i += QT4) s_s[i] = xs[i];
+    for (int i = threadIdx.x; i < kTok4 * cols / 16; i += QT4) s_s[i] = (float)xs[i];
     __syncthreads();
 
     constexpr int WAVES4 = QT4 / 64;

@@ -13,7 +13,12 @@
 //    session.  Every workgroup does at most that share whatever
 //    the context lengths, so
 //    a ragged batch fills all CUs evenly, and a workgroup never straddles two
-//    sessions.  Each workgroup writes one partial (m, l, acc[HD]) per head.
+//    sessions.  Each workgroup writes one partial (m, l, acc[HD]) per head
+//    and wave row in the batched path (the combine merges the wave rows with
+//    the workgroups: measured 0.8465 -> 0.8345 ms per config-2 step against
+//    merging them in LDS behind a barrier first, although the partial bytes
+//    double), one per head in the reference-signature path (its scratch holds
+//    32 rows per head).
 //    Every wave derives the partition itself from one load of n_keys.
 //  * One workgroup = 8 wave64s, one workgroup per CU.  Wave w serves kv head
 //    w % NKV and takes every R-th pair of pages (R = 8/NKV), so the workgroup
@@ -96,9 +101,10 @@ struct DecodeArgs {
     const float* v_new32;
     const float* cs;         // RoPE table rows [pos][HD/2] (null: no rotation)
     const float* sn;
-    float* part;             // [(Gw + n_sess)][NH][PW]
+    float* part;             // [(Gw + n_sess) * (wave_parts ? R : 1)][NH][PW]
     const int32_t* plan;     // per-step plan (null: derive the partition in-kernel)
     int gw;                  // workgroups in the grid
+    int wave_parts;          // 1: a partial slot per (workgroup, wave row), no in-workgroup merge
 };
 
 // Per-step plan, written once per decode step by decode_plan_kernel (n_keys
@@ -512,9 +518,8 @@ decode_split_kernel(DecodeArgs a) {
 
         lsum += shfl_xor_f(lsum, 16);
         lsum += shfl_xor_f(lsum, 32);
-        float* pout = a.part + (int64_t)w * NH * PW;
-        if constexpr (R == 1) {
-            // one wave per kv head: its registers are the partial
+        // this wave's G rows of a partial slot, straight from the accumulators
+        auto write_rows = [&](float* pout) {
             if (c < G) {
                 float* row = pout + (int64_t)(kvh * G + c) * PW;
                 if (g == 0) {
@@ -537,8 +542,15 @@ decode_split_kernel(DecodeArgs a) {
                     }
                 }
             }
+        };
+        if constexpr (R == 1) {
+            write_rows(a.part + (int64_t)w * NH * PW);
+        } else if (a.wave_parts) {
+            // slot w*R + r: the combine merges the R rows with the workgroups'
+            write_rows(a.part + ((int64_t)w * R + r) * NH * PW);
         } else {
             // merge the R waves of each kv head in LDS
+            float* pout = a.part + (int64_t)w * NH * PW;
             if (g == 0) {
                 s_m[wave][c] = m;
                 s_l[wave][c] = lsum;
@@ -618,6 +630,9 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     }
     constexpr int64_t SEG = (int64_t)NH * PW;
     constexpr int kChunk = 8;
+    const int rows = a.wave_parts ? R : 1;         // partial slots per split workgroup
+    pt.kc *= rows;
+    pt.k *= rows;
     const float* base = a.part + (int64_t)pt.kc * SEG + (int64_t)h * PW;
     float M = -INFINITY, L = 0.f;
     f4 A = {0.f, 0.f, 0.f, 0.f};
@@ -765,6 +780,7 @@ DecodeArgs batch_args(const int32_t* tables, int table_stride, const int32_t* n_
     a.gw = batch_workgroups();
     a.plan = static_cast<const int32_t*>(workspace);
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan_bytes(n_sess));
+    a.wave_parts = 1;
     return a;
 }
 
@@ -777,7 +793,7 @@ extern "C" {
 
 size_t attn_decode_batch_workspace_bytes(int n_sess) {
     NOVA_REQUIRE(n_sess >= 1 && n_sess <= kMaxBatch);
-    return plan_bytes(n_sess) + (size_t)(batch_workgroups() + n_sess) * NH * PW * sizeof(float);
+    return plan_bytes(n_sess) + (size_t)(batch_workgroups() + n_sess) * R * NH * PW * sizeof(float);
 }
 
 void launch_attn_decode_plan(const int32_t* tables, int table_stride, const int32_t* n_keys, int n_sess,

@@ -53,6 +53,8 @@ def parse():
                     choices=["decode7b", "single1p5b", "cow", "longctx14b", "prefill", "rope", "gemv", "copycal"])
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--main-only", action="store_true",
+                    help="decode workloads: time the batched step only (no per-session or fused-RoPE comparison legs)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
     return ap.parse_args()
 
@@ -299,6 +301,7 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
     nova = nova_amd.load(model)
     s = nova.dev_stream_create()
     wl = DecodeWorkload(nova, ctx, args.seed, s)
+    print("[leg] batched step", file=sys.stderr, flush=True)
     wl.step_eager()            # first touch, check launches
     nova.dev_stream_sync(s)
     wl.capture()
@@ -339,8 +342,13 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
                          f"{secs:.2f} s; max|gpu-cpu| on that layer {err:.2e}",
                "us_per_step_equiv": round(secs * wl.layers * 1e6, 1)}
     # after the parity leg above: they rewrite the outputs and the appended slots
-    per_session = wl.per_session_ms(args.steps, args.warmup)
-    rope = wl.rope_compare(args.steps, args.warmup) if model == "qwen25_7b" else None
+    per_session = rope = None
+    if not getattr(args, "main_only", False):
+        print("[leg] per-session launches", file=sys.stderr, flush=True)
+        per_session = wl.per_session_ms(args.steps, args.warmup)
+        if model == "qwen25_7b":
+            print("[leg] rope in step", file=sys.stderr, flush=True)
+            rope = wl.rope_compare(args.steps, args.warmup)
     line = {
         "metric": metric_cfg["metric"], "value": round(gbs, 2), "unit": "GB/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
@@ -351,10 +359,11 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
     }
     if parity:
         line["parity"] = parity
-    line["per_session_launches"] = {
-        "ms_per_step": round(per_session, 4), "GBs": round(bytes_step / (per_session * 1e-3) / 1e9, 1),
-        "what": "the same step as the reference calls it: per layer and session launch_kv_store_paged + "
-                "launch_attn_decode_paged (2N launches per layer), from a HIP graph"}
+    if per_session:
+        line["per_session_launches"] = {
+            "ms_per_step": round(per_session, 4), "GBs": round(bytes_step / (per_session * 1e-3) / 1e9, 1),
+            "what": "the same step as the reference calls it: per layer and session launch_kv_store_paged + "
+                    "launch_attn_decode_paged (2N launches per layer), from a HIP graph"}
     if rope:
         line["rope_in_step"] = dict(rope, note="the same step with RoPE of q and the new k in front of each layer: "
                                                "launch_rope_kv_store_paged_batch + planned decode, against "

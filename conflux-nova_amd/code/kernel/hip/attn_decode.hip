@@ -121,12 +121,14 @@ __host__ __device__ constexpr int64_t plan_ints(int n_sess, int gw) {
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
-// K/V page loads.  V goes out non-temporal: every lane group reads whole
-// 256 B row slices, each byte once per launch (measured: the config-2 step
-// 0.905 -> 0.875 ms; page-sized non-temporal streaming reaches 6.9 TB/s
-// against 6.1 TB/s on this part).  K keeps the default policy: one K load
-// reads 64 B of each of 16 rows, half a 128 B line, and the next load the
-// other half, which non-temporal loads do not keep (measured 0.97 ms).
+// K/V page loads go out non-temporal: each byte is read once per launch, and
+// every load instruction covers whole 128 B lines (V: 256 B row slices; K:
+// 8 rows x 128 B, see k_operand).  Measured: page-sized non-temporal
+// streaming reaches 6.9 TB/s against 6.1 TB/s with the default policy; V
+// non-temporal took the config-2 step 0.905 -> 0.875 ms, K with whole-line
+// loads 0.834-0.841 -> 0.826 ms (config 4: 6.21 -> 6.37-6.55 TB/s).  K
+// loaded the MFMA's way (64 B of 16 rows per instruction, the other half of
+// each line by the next one) is slower non-temporal: 0.97 ms.
 __device__ __forceinline__ u4 ld16(const char* base, uint32_t off) {
     return *reinterpret_cast<const u4*>(base + off);
 }
@@ -233,9 +235,29 @@ __device__ Part partition(const DecodeArgs& a, int w, int want) {
 
 // K and V operands of one pair of pages, as loaded
 struct PairRegs {
-    u4 k0[4], k1[4];   // K rows c of page 0 / page 1, halves [32ks + 8g, +8)
+    u4 k0[4], k1[4];   // K of page 0 / page 1 as whole-line loads (k_operand)
     u4 v[8];           // V rows kappa(g,j) = (page j/4, slot 4g + j%4), halves [8c, +8)
 };
+
+// K operand ks of one page from the whole-line loads.  Load 2h+0 (X) holds,
+// in lane (g,c), row c&7 at bytes 128h + 16(g + 4(c>>3)); load 2h+1 (Y) the
+// same for rows 8 + (c&7).  The MFMA wants row c at bytes 64ks + 16g: for
+// even ks that is X in lanes c < 8 and Y of lane c-8 in lanes c >= 8; for odd
+// ks, X of lane c+8 in lanes c < 8 and Y in lanes c >= 8.  A row_ror:8 DPP
+// move writing only the banks (4-lane groups) of the lanes that need it
+// builds each operand dword in one instruction.
+__device__ __forceinline__ u4 k_operand(const u4* kl, int ks) {
+    const u4 x = kl[ks & 2], y = kl[(ks & 2) + 1];
+    u4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (ks & 1)
+            r[e] = (uint32_t)__builtin_amdgcn_update_dpp((int)y[e], (int)x[e], 0x128, 0xF, 0x3, false);
+        else
+            r[e] = (uint32_t)__builtin_amdgcn_update_dpp((int)x[e], (int)y[e], 0x128, 0xF, 0xC, false);
+    }
+    return r;
+}
 
 template <bool kRope>
 __global__ void __launch_bounds__(THREADS)
@@ -280,7 +302,7 @@ decode_split_kernel(DecodeArgs a) {
     const int32_t* table = a.tables + (int64_t)i * a.table_stride;
 
     // lane-constant byte offsets inside a page
-    const uint32_t koff = (uint32_t)(c * kRowBytes + kvh * HD * 2 + 16 * g);
+    const uint32_t koff = (uint32_t)((c & 7) * kRowBytes + kvh * HD * 2 + 16 * (g + 4 * (c >> 3)));
     uint32_t voff[4];
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) voff[jj] = (uint32_t)((4 * g + jj) * kRowBytes + kvh * HD * 2 + 16 * c);
@@ -314,8 +336,9 @@ decode_split_kernel(DecodeArgs a) {
             const char* v1 = pv + b1;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                pr.k0[ks] = ld16(k0, koff + 64 * ks);
-                pr.k1[ks] = ld16(k1, koff + 64 * ks);
+                const uint32_t o = koff + (ks & 1) * 8 * kRowBytes + (ks >> 1) * 128;
+                pr.k0[ks] = ld16_nt(k0, o);
+                pr.k1[ks] = ld16_nt(k1, o);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -443,8 +466,8 @@ decode_split_kernel(DecodeArgs a) {
             f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const h8 ka = __builtin_bit_cast(h8, cur.k0[ks]);
-                const h8 kc = __builtin_bit_cast(h8, cur.k1[ks]);
+                const h8 ka = __builtin_bit_cast(h8, k_operand(cur.k0, ks));
+                const h8 kc = __builtin_bit_cast(h8, k_operand(cur.k1, ks));
                 const h8 qhi = __builtin_bit_cast(h8, s_q[kvh][ks][0][lane]);
                 const h8 qlo = __builtin_bit_cast(h8, s_q[kvh][ks][1][lane]);
                 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi, s0, 0, 0, 0);

@@ -38,6 +38,9 @@ namespace {
 
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef int32_t i4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 constexpr int kQK = 256;                       // weights per super-block
 constexpr int kBlockBytes = 144;
@@ -238,7 +241,49 @@ __device__ __forceinline__ int mat_of(const GemvSet& g, int64_t r) {
 // The activation (codes, scales per 32, sums per 16) into LDS, once per
 // workgroup; from ActQ8 as given, or quantised here from fp32.  The sums are
 // kept as floats (exact: |sum| <= 16 * 127), so no dot product converts them.
-template <bool kF32>
+// Copies an ActQ8 activation of n columns (codes, per-32 scales, per-16
+// sums, the sums converted to exact floats) into LDS; NT threads, n <= MAXC.
+// The loads of a round all go out before its LDS stores: a strided copy loop
+// waits out one load latency per element, which at the FFN width was 3 us of
+// the down projection's 11.4.  Codes go in rounds of 8 x 16 B per thread, the
+// sums and scales as 16 B loads with the first round.  No barrier.
+template <int NT, int MAXC>
+__device__ __forceinline__ void stage_q8(const int8_t* xq, const float* xd, const int32_t* xs, int n, int8_t* s_q,
+                                         float* s_d, float* s_s) {
+    constexpr int NQ = (MAXC / 16 + NT - 1) / NT < 8 ? (MAXC / 16 + NT - 1) / NT : 8;
+    constexpr int NS = (MAXC / 64 + NT - 1) / NT;
+    constexpr int ND = (MAXC / 128 + NT - 1) / NT;
+    const int t = threadIdx.x;
+    i4 vs[NS];
+    f4 vd[ND];
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+        if (t + k * NT < n / 64) vs[k] = *reinterpret_cast<const i4*>(xs + 4 * (t + k * NT));
+#pragma unroll
+    for (int k = 0; k < ND; ++k)
+        if (t + k * NT < n / 128) vd[k] = *reinterpret_cast<const f4*>(xd + 4 * (t + k * NT));
+#pragma unroll 1
+    for (int b = t; b < n / 16; b += NQ * NT) {
+        u4 vq[NQ];
+#pragma unroll
+        for (int k = 0; k < NQ; ++k)
+            if (b + k * NT < n / 16) vq[k] = *reinterpret_cast<const u4*>(xq + 16 * (b + k * NT));
+#pragma unroll
+        for (int k = 0; k < NQ; ++k)
+            if (b + k * NT < n / 16) *reinterpret_cast<u4*>(s_q + 16 * (b + k * NT)) = vq[k];
+    }
+#pragma unroll
+    for (int k = 0; k < NS; ++k)
+        if (t + k * NT < n / 64) {
+            const i4 v = vs[k];
+            *reinterpret_cast<f4*>(s_s + 4 * (t + k * NT)) = f4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+        }
+#pragma unroll
+    for (int k = 0; k < ND; ++k)
+        if (t + k * NT < n / 128) *reinterpret_cast<f4*>(s_d + 4 * (t + k * NT)) = vd[k];
+}
+
+template <bool kF32, int MAXC = kMaxCols>
 __device__ __forceinline__ void stage_activation(const GemvSet& g, int8_t* s_q, float* s_d, float* s_s) {
     const int cols = g.cols;
     if constexpr (kF32) {
@@ -254,15 +299,12 @@ __device__ __forceinline__ void stage_activation(const GemvSet& g, int8_t* s_q, 
             s_s[2 * b + 1] = (float)s1;
         }
     } else {
-        for (int i = threadIdx.x; i < cols / 16; i += QT)
-            *reinterpret_cast<u4*>(s_q + 16 * i) = *reinterpret_cast<const u4*>(g.xq + 16 * i);
-        for (int i = threadIdx.x; i < cols / 32; i += QT) s_d[i] = g.xd[i];
-        for (int i = threadIdx.x; i < cols / 16; i += QT) s_s[i] = (float)g.xs[i];
+        stage_q8<QT, MAXC>(g.xq, g.xd, g.xs, cols, s_q, s_d, s_s);
     }
     __syncthreads();
 }
 
-// Rows of at most 4 steps (8 super-blocks per step, cols <= 8192): the step
+// Rows of at most 4 steps (16 super-blocks per step, cols <= 16384): the step
 // loop is unrolled at compile time, one row per wave, all of the row's loads
 // issued before any is consumed.  (Measured on gfx950: taking 2 or 4 rows per
 // wave at once, or loading the next row while the current one is reduced,
@@ -275,7 +317,7 @@ __global__ void __launch_bounds__(QT) gemv_fixed_kernel(GemvSet g) {
     int8_t* s_q = reinterpret_cast<int8_t*>(s_x);
     float* s_d = reinterpret_cast<float*>(s_x + cols);
     float* s_s = reinterpret_cast<float*>(s_x + cols + 4 * (cols / 32));   // 16-sums as exact floats
-    stage_activation<kF32>(g, s_q, s_d, s_s);
+    stage_activation<kF32, STEPS * Lanes<kLps1>::kSbPerStep * kQK>(g, s_q, s_d, s_s);
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar row addressing
@@ -326,7 +368,7 @@ __global__ void __launch_bounds__(QT) gemv_split_kernel(GemvSet g) {
     int8_t* s_q = reinterpret_cast<int8_t*>(s_x);
     float* s_d = reinterpret_cast<float*>(s_x + cols);
     float* s_s = reinterpret_cast<float*>(s_x + cols + 4 * (cols / 32));   // 16-sums as exact floats
-    stage_activation<kF32>(g, s_q, s_d, s_s);
+    stage_activation<kF32, (STEPS * Lanes<kLps1>::kSbPerStep * kQK * KS < kMaxCols ? STEPS * Lanes<kLps1>::kSbPerStep * kQK * KS : kMaxCols)>(g, s_q, s_d, s_s);
 
     constexpr int RPI = 4 / KS;
     const int lane = threadIdx.x & 63;
@@ -400,10 +442,7 @@ __global__ void __launch_bounds__(QT4) gemv4_kernel(const uint8_t* __restrict__ 
     int8_t* s_q = reinterpret_cast<int8_t*>(s_x);                                   // [4][cols]
     float* s_d = reinterpret_cast<float*>(s_x + kTok4 * cols);                       // [4][cols/32]
     float* s_s = reinterpret_cast<float*>(s_x + kTok4 * cols + 4 * kTok4 * (cols / 32));   // [4][cols/16]
-    for (int i = threadIdx.x; i < kTok4 * cols / 16; i += QT4)
-        *reinterpret_cast<u4*>(s_q + 16 * i) = *reinterpret_cast<const u4*>(xq + 16 * i);
-    for (int i = threadIdx.x; i < kTok4 * cols / 32; i += QT4) s_d[i] = xd[i];
-    for (int i = threadIdx.x; i < kTok4 * cols / 16; i += QT4) s_s[i] = (float)xs[i];
+    stage_q8<QT4, kTok4 * kMaxCols4>(xq, xd, xs, kTok4 * cols, s_q, s_d, s_s);
     __syncthreads();
 
     constexpr int WAVES4 = QT4 / 64;
@@ -552,6 +591,7 @@ void launch_gemv_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_t
                      const int32_t* xs, float* out, nova_stream_t s) {
     NOVA_REQUIRE(blocks && xq && xd && xs && out && rows >= 0);
     NOVA_REQUIRE(cols > 0 && cols % kQK == 0 && cols <= kMaxCols);
+    NOVA_REQUIRE(aligned16(xq) && aligned16(xd) && aligned16(xs));   // staged with 16 B loads
     if (rows == 0) return;
     GemvSet g{};
     g.w[0] = blocks;
@@ -569,6 +609,7 @@ void launch_gemv4_q4k(const uint8_t* blocks, int64_t rows, int cols, const int8_
                       const int32_t* xs, float* out, nova_stream_t s) {
     NOVA_REQUIRE(blocks && xq && xd && xs && out && rows >= 0);
     NOVA_REQUIRE(cols > 0 && cols % kQK == 0 && cols <= kMaxCols4);
+    NOVA_REQUIRE(aligned16(xq) && aligned16(xd) && aligned16(xs));   // staged with 16 B loads
     if (rows == 0) return;
     const size_t lds = kTok4 * ((size_t)cols + 4 * (size_t)(cols / 32) + 4 * (size_t)(cols / 16));
     const hipStream_t st = reinterpret_cast<hipStream_t>(s);

@@ -191,7 +191,10 @@ void launch_rope_kv_store_paged_batch(float* q, const float* k, const float* v, 
  * (include/nova/quant/q4_k.h:19-25: 144 B per 256 weights, row-major,
  * rows x cols/256 blocks), activations as ActQ8 (include/nova/kernel/types.h:24-28)
  * passed as three plain arrays: int8 codes [rows][cols], fp32 scales
- * [rows][cols/32], int32 sums of each 16 codes [rows][cols/16]. ---- */
+ * [rows][cols/32], int32 sums of each 16 codes [rows][cols/16].  The GEMVs
+ * read the three activation arrays with 16-byte loads and abort on pointers
+ * that are not 16-byte aligned (the reference's ActQ8 buffers come from its
+ * arena, which aligns them). ---- */
 
 /* Quantise rows x cols fp32 activations (cols % 32 == 0).  Replaces
  * nova::launch_quant / launch_quant_ffn, q4k_gemv.cu:196-207 (kernel :9-33),

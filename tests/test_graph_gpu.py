@@ -172,3 +172,28 @@ def test_gemv_fused_graph(nova7):
     assert np.all(np.isfinite(eager))
     for r, got in enumerate(reps):
         assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"
+
+
+def test_gemv4_mfma_graph(nova7):
+    """the four-token GEMV on its matrix-core path (32M weights and up), ragged 16-row blocks"""
+    nova = nova7
+    print("[case] graph gemv4 mfma", flush=True)
+    rng = np.random.default_rng(9)
+    rows, cols = 2051, 16384
+    b = rng.integers(0, 256, (rows, cols // 256, 144), dtype=np.uint8)
+    b[..., 0:2] = rng.uniform(2e-4, 4e-3, (rows, cols // 256, 1)).astype(np.float16).view(np.uint8)
+    b[..., 2:4] = rng.uniform(1e-4, 2e-3, (rows, cols // 256, 1)).astype(np.float16).view(np.uint8)
+    w = nova.upload(b)
+    x4 = nova.upload(rng.standard_normal((4, cols)).astype(np.float32))
+    qs, dd, sm = nova.alloc(4 * cols), nova.alloc(4 * cols // 8), nova.alloc(4 * cols // 4)
+    out4 = nova.alloc(4 * rows * 4)
+    s = nova.dev_stream_create()
+
+    def run():
+        nova.launch_quant_q8(qs.ptr, dd.ptr, sm.ptr, x4.ptr, 4, cols, s)
+        nova.launch_gemv4_q4k(w.ptr, rows, cols, qs.ptr, dd.ptr, sm.ptr, out4.ptr, s)
+
+    eager, reps = _replays(nova, s, run, lambda: out4.numpy((4 * rows,), np.float32))
+    assert np.all(np.isfinite(eager))
+    for r, got in enumerate(reps):
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"

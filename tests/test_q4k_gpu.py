@@ -113,7 +113,9 @@ def test_gemv_f32_fused(cols, rows, nova7, oracle):
 
 
 @pytest.mark.parametrize("rows,cols", [(37, 256), (512, 3584), (3584, 3584), (130, 18944), (70, 8960),
-                                       (33, 13824), (5, 28672), (1, 1536)])
+                                       (33, 13824), (5, 28672), (1, 1536),
+                                       # 32M weights and up: the MFMA kernel (ragged 16-row blocks too)
+                                       (2051, 16384), (20001, 2048), (18944, 3584), (3584, 18944)])
 def test_gemv4_matches_single_token(rows, cols, nova7, oracle):
     """launch_gemv4_q4k (4 stacked tokens, one weight read): every token's
     output within the GEMV tolerance of the oracle, and of launch_gemv_q4k on
@@ -137,11 +139,12 @@ def test_gemv4_matches_single_token(rows, cols, nova7, oracle):
         singles.append(o1)
     nova.dev_sync()
     got = out4.numpy((4, rows), np.float32)
-    check = slice(None) if rows <= 600 else slice(0, rows, max(rows // 300, 1))
+    # every row up to 600, else ~300 spread rows and the last 17 (a ragged last 16-row block)
+    check = np.arange(rows) if rows <= 600 else np.unique(np.r_[np.arange(0, rows, rows // 300), np.arange(rows - 17, rows)])
     for t in range(4):
         one = singles[t].numpy((rows,), np.float32)
         ref = oracle.gemv_q4k(w, rows, cols, qs[t:t + 1], d[t:t + 1], s[t:t + 1])
-        scale = abs_terms(oracle, w[check], len(range(rows)[check]), cols, qs[t:t + 1], d[t:t + 1])
+        scale = abs_terms(oracle, w[check], len(check), cols, qs[t:t + 1], d[t:t + 1])
         err = np.abs(got[t][check].astype(np.float64) - ref[check])
         assert np.all(err <= 2e-6 * scale), f"token {t}: max err/scale {np.max(err / scale):.2e}"
         diff = np.abs(got[t][check].astype(np.float64) - one[check])

@@ -76,6 +76,8 @@ def _abort_run(code):
     ("n.launch_gemv_q4k(1, 4, 65536, 1, 1, 1, 1, None)", "cols <= kMaxCols"),
     ("n.launch_quant_q8(1, 1, 1, 1, 1, 33, None)", "cols % 32 == 0"),
     ("n.launch_gemv4_q4k(1, 4, 28928, 1, 1, 1, 1, None)", "cols <= kMaxCols4"),
+    ("n.launch_gemv_q4k(1, 4, 256, 256, 260, 512, 1, None)", "aligned16(xd)"),
+    ("n.launch_gemv4_q4k(1, 4, 256, 264, 256, 512, 1, None)", "aligned16(xq)"),
     ("n.launch_attn_decode_paged_rope_planned(1, 1, 1, None, 1, 1, 1, 1, 1, 1, 0, 4, 1, 1, None)",
      "q && k_new && v_new && cs && sn"),
     ("n.launch_attn_decode_paged_rope_planned(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 28, 4, 1, 1, None)",

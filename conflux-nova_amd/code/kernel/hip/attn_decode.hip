@@ -18,7 +18,8 @@
 //    the workgroups: measured 0.8465 -> 0.8345 ms per config-2 step against
 //    merging them in LDS behind a barrier first, although the partial bytes
 //    double), one per head in the reference-signature path (its scratch holds
-//    32 rows per head).
+//    32 rows per head; there each page range runs as NKV workgroups, one per
+//    kv head, so one single-session call spreads over 31 * NKV CUs).
 //    Every wave derives the partition itself from one load of n_keys.
 //  * One workgroup = 8 wave64s, one workgroup per CU.  Wave w serves kv head
 //    w % NKV and takes every R-th pair of pages (R = 8/NKV), so the workgroup
@@ -105,6 +106,7 @@ struct DecodeArgs {
     const int32_t* plan;     // per-step plan (null: derive the partition in-kernel)
     int gw;                  // workgroups in the grid
     int wave_parts;          // 1: a partial slot per (workgroup, wave row), no in-workgroup merge
+    int kv_split;            // 1: grid.y = kv head, all waves of a workgroup on that head (no fused append)
 };
 
 // Per-step plan, written once per decode step by decode_plan_kernel (n_keys
@@ -261,12 +263,12 @@ __device__ __forceinline__ u4 k_operand(const u4* kl, int ks) {
     return r;
 }
 
-template <bool kRope>
+template <bool kRope, bool kKvSplit>
 __global__ void __launch_bounds__(THREADS)
 decode_split_kernel(DecodeArgs a) {
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];
-    __shared__ float s_acc[R > 1 ? WAVES : 1][G][HD];
+    __shared__ float s_acc[(R > 1 || kKvSplit) ? WAVES : 1][G][HD];
     __shared__ u4 s_q[NKV][4][2][64];            // Q^T hi/lo operands per kv head
     __shared__ float s_qf[NKV][16];              // per-head score factor
 
@@ -275,8 +277,11 @@ decode_split_kernel(DecodeArgs a) {
     const int lane = tid & 63;
     const int g = lane >> 4;      // 0..3
     const int c = lane & 15;      // 0..15
-    const int kvh = wave % NKV;
-    const int r = wave / NKV;
+    // kv-split: workgroup (w, kv head) streams that head's rows of its page
+    // range with all waves; otherwise wave w serves kv head w % NKV
+    const int kvh = kKvSplit ? (int)blockIdx.y : wave % NKV;
+    const int r = kKvSplit ? wave : wave / NKV;
+    constexpr int RS = kKvSplit ? WAVES : R;        // waves per kv head = pair stride
     const int w = blockIdx.x;
 
     int i, n_keys, pa, pb, tv;
@@ -536,7 +541,7 @@ decode_split_kernel(DecodeArgs a) {
         // each wave keeps one pair (16 KiB) in flight; the 8 waves of the CU
         // overlap each other's latency (measured: a register ping-pong of two
         // pairs per wave, with Q re-read from LDS to fit 256 VGPRs, is slower)
-        for (int qp = r; qp < npairs; qp += R) {
+        for (int qp = r; qp < npairs; qp += RS) {
             if (qp != r || !early) load_pair(qp, cur);
             compute_pair(qp, cur);
         }
@@ -568,13 +573,14 @@ decode_split_kernel(DecodeArgs a) {
                 }
             }
         };
-        if constexpr (R == 1) {
+        if constexpr (R == 1 && !kKvSplit) {
             write_rows(a.part + (int64_t)w * NH * PW);
         } else if (a.wave_parts) {
             // slot w*R + r: the combine merges the R rows with the workgroups'
             write_rows(a.part + ((int64_t)w * R + r) * NH * PW);
         } else {
-            // merge the R waves of each kv head in LDS
+            // merge the waves of each kv head in LDS (kv-split: the G heads of
+            // this workgroup's kv head over all its waves)
             float* pout = a.part + (int64_t)w * NH * PW;
             if (g == 0) {
                 s_m[wave][c] = m;
@@ -594,16 +600,20 @@ decode_split_kernel(DecodeArgs a) {
                 }
             }
             __syncthreads();
-            for (int idx = tid; idx < NH * HD; idx += THREADS) {
-                const int h = idx / HD, d = idx - h * HD;
+            const int h0 = kKvSplit ? kvh * G : 0;
+            constexpr int n_out = kKvSplit ? G * HD : NH * HD;
+            for (int idx = tid; idx < n_out; idx += THREADS) {
+                const int h = h0 + idx / HD, d = idx - (idx / HD) * HD;
                 const int hk = h / G, hc = h - hk * G;
                 float M = -INFINITY;
 #pragma unroll
-                for (int rr = 0; rr < R; ++rr) M = fmaxf(M, s_m[hk + NKV * rr][hc]);
+                for (int rr = 0; rr < WAVES; ++rr)
+                    if (rr < RS) M = fmaxf(M, s_m[kKvSplit ? rr : hk + NKV * rr][hc]);
                 float L = 0.f, A = 0.f;
 #pragma unroll
-                for (int rr = 0; rr < R; ++rr) {
-                    const int ww = hk + NKV * rr;
+                for (int rr = 0; rr < WAVES; ++rr) {
+                    if (rr >= RS) break;
+                    const int ww = kKvSplit ? rr : hk + NKV * rr;
                     const float lw = s_l[ww][hc];
                     const float f = lw > 0.f ? exp2f(s_m[ww][hc] - M) : 0.f;
                     L = fmaf(lw, f, L);
@@ -784,8 +794,10 @@ int batch_workgroups() {
 }
 
 void launch_pair(const DecodeArgs& a, int n_sess, float* o, hipStream_t st) {
-    if (a.cs) hipLaunchKernelGGL(decode_split_kernel<true>, dim3(a.gw + n_sess), dim3(THREADS), 0, st, a);
-    else hipLaunchKernelGGL(decode_split_kernel<false>, dim3(a.gw + n_sess), dim3(THREADS), 0, st, a);
+    const dim3 grid(a.gw + n_sess, a.kv_split ? NKV : 1);
+    if (a.kv_split) hipLaunchKernelGGL((decode_split_kernel<false, true>), grid, dim3(THREADS), 0, st, a);
+    else if (a.cs) hipLaunchKernelGGL((decode_split_kernel<true, false>), grid, dim3(THREADS), 0, st, a);
+    else hipLaunchKernelGGL((decode_split_kernel<false, false>), grid, dim3(THREADS), 0, st, a);
     NOVA_LAUNCHED();
     hipLaunchKernelGGL(decode_combine_kernel, dim3(n_sess, NH), dim3(CT), 0, st, a, o);
     NOVA_LAUNCHED();
@@ -910,6 +922,7 @@ void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint
     a.nb = nb;
     a.part = scratch;
     a.gw = gw;
+    a.kv_split = 1;   // NKV workgroups per partial slot: 31 * NKV CUs per call
     launch_pair(a, 1, o, reinterpret_cast<hipStream_t>(s));
 }
 

@@ -117,8 +117,24 @@ struct DecodeArgs {
 // n_keys -> partition -> block-table chain.
 constexpr int kRecPages = 64;
 constexpr int kRec = kRecPages + 4;
+// Workgroup slots and XCDs.  Workgroup w runs on XCD w % 8.  The first
+// 8 * ceil(gw / 8) slots take the workgroups' logical indices XCD by XCD
+// (logical L = (w % 8) * per + w / 8), so a session's workgroups, which are
+// consecutive logical indices, share one or two XCDs and their partial rows
+// stay in those XCDs' L2 for the combine; slots past those map to themselves
+// (only used when the sessions outnumber what one round of gw workgroups can
+// split).
+__host__ __device__ constexpr int xcd_per(int gw) { return (gw + 7) / 8; }
+__host__ __device__ constexpr int split_slots(int n_sess, int gw) { return 8 * xcd_per(gw) + n_sess; }
+__host__ __device__ __forceinline__ int logical_of(int w, int gw) {
+    const int per = xcd_per(gw);
+    return w < 8 * per ? (w & 7) * per + (w >> 3) : w;
+}
+// plan: [session table n_sess x 4 | combine map n_sess*NH x 4 | records]
+__host__ __device__ constexpr int64_t plan_map_off(int n_sess) { return (int64_t)n_sess * 4; }
+__host__ __device__ constexpr int64_t plan_rec_off(int n_sess) { return (int64_t)n_sess * 4 + (int64_t)n_sess * NH * 4; }
 __host__ __device__ constexpr int64_t plan_ints(int n_sess, int gw) {
-    return (int64_t)n_sess * 4 + (int64_t)(gw + n_sess) * kRec;
+    return plan_rec_off(n_sess) + (int64_t)split_slots(n_sess, gw) * kRec;
 }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
@@ -287,7 +303,7 @@ decode_split_kernel(DecodeArgs a) {
     int i, n_keys, pa, pb, tv;
     if (a.plan) {
         // one load: lane t holds phys[t]; lanes 0..3 the header
-        const int32_t* rec = a.plan + (int64_t)a.n_sess * 4 + (int64_t)w * kRec;
+        const int32_t* rec = a.plan + plan_rec_off(a.n_sess) + (int64_t)w * kRec;
         tv = rec[lane];
         const int hv = rec[kRecPages + (lane & 3)];
         i = __builtin_amdgcn_readlane(hv, 0);
@@ -574,10 +590,10 @@ decode_split_kernel(DecodeArgs a) {
             }
         };
         if constexpr (R == 1 && !kKvSplit) {
-            write_rows(a.part + (int64_t)w * NH * PW);
+            write_rows(a.part + (int64_t)(a.plan ? logical_of(w, a.gw) : w) * NH * PW);
         } else if (a.wave_parts) {
             // slot w*R + r: the combine merges the R rows with the workgroups'
-            write_rows(a.part + ((int64_t)w * R + r) * NH * PW);
+            write_rows(a.part + ((int64_t)(a.plan ? logical_of(w, a.gw) : w) * R + r) * NH * PW);
         } else {
             // merge the waves of each kv head in LDS (kv-split: the G heads of
             // this workgroup's kv head over all its waves)
@@ -643,19 +659,23 @@ constexpr int kCombGroups = CT / (HD / 4);
 
 __global__ void __launch_bounds__(CT)
 decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
-    const int i = blockIdx.x, h = blockIdx.y;
+    const int t = blockIdx.x;
+    int i, h;
     const int tid = threadIdx.x, g = tid / (HD / 4), q4 = tid - g * (HD / 4);
     __shared__ float s_m[kCombGroups], s_l[kCombGroups];
     __shared__ f4 s_a[kCombGroups][HD / 4];
     Part pt;
     if (a.plan) {
-        const int32_t* e = a.plan + (int64_t)i * 4;     // {kc, k, n_keys, pages}
+        // block t (XCD t % 8) serves the (session, head) the plan placed on it
+        const int4 e = *reinterpret_cast<const int4*>(a.plan + plan_map_off(a.n_sess) + (int64_t)t * 4);
+        pt.kc = e.x;
+        pt.k = e.y;
+        i = e.z;
+        h = e.w;
         pt.sess = i;
-        pt.kc = e[0];
-        pt.k = e[1];
-        pt.n_keys = e[2];
-        pt.pages = e[3];
     } else {
+        i = t % a.n_sess;
+        h = t / a.n_sess;
         pt = partition(a, 0, i);
     }
     f4* orow = reinterpret_cast<f4*>(o + ((int64_t)i * NH + h) * HD) + q4;
@@ -721,13 +741,15 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     *orow = Ax * inv;
 }
 
-// Per-step plan: block w (< gw + n_sess) writes the record of workgroup slot w;
-// the last block also writes the session table.  64 threads per block.
+// Per-step plan: block w (< split_slots) writes the record of workgroup slot w;
+// the last block also writes the session table and the combine map.  64
+// threads per block.
 __global__ void __launch_bounds__(64)
 decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
     const int w = blockIdx.x, lane = threadIdx.x;
-    const int n_slots = a.gw + a.n_sess;
+    const int n_slots = split_slots(a.n_sess, a.gw);
     if (w == n_slots) {
+        __shared__ int s_kc[kMaxBatch], s_k[kMaxBatch], s_home[kMaxBatch], s_rank[kMaxBatch];
         // session table: the same prefix as partition(), one lane per session
         int T = 0;
         for (int base = 0; base < a.n_sess; base += 64) {
@@ -753,22 +775,70 @@ decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
             }
             if (ii < a.n_sess) {
                 int32_t* e = plan + (int64_t)ii * 4;
-                e[0] = carry + incl - k;
+                const int kc = carry + incl - k;
+                e[0] = kc;
                 e[1] = k;
                 e[2] = nk;
                 e[3] = pg;
+                s_kc[ii] = kc;
+                s_k[ii] = k;
+                // home XCD: the one that runs the session's middle workgroup
+                const int per = xcd_per(a.gw);
+                const int mid = kc + (k > 0 ? (k - 1) / 2 : 0);
+                s_home[ii] = mid < 8 * per ? mid / per : 0;
             }
             carry += __shfl(incl, 63, 64);
         }
+        // combine map: block t runs on XCD t % 8; each XCD first takes the
+        // (session, head) pairs of its own sessions, the overflow fills the
+        // blocks other XCDs leave free
+        __shared__ int s_cap[8], s_dem[8], s_ovpre[8], s_freepre[8];
+        __syncthreads();
+        const int NT = a.n_sess * NH;
+        if (lane == 0) {
+            int cnt[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int ii = 0; ii < a.n_sess; ++ii) s_rank[ii] = cnt[s_home[ii]]++;
+            int ov = 0, fr = 0;
+            for (int x = 0; x < 8; ++x) {
+                const int cap = NT > x ? (NT - x + 7) / 8 : 0;
+                const int dem = NH * cnt[x];
+                s_cap[x] = cap;
+                s_dem[x] = dem;
+                s_ovpre[x] = ov;
+                s_freepre[x] = fr;
+                ov += dem > cap ? dem - cap : 0;
+                fr += cap > dem ? cap - dem : 0;
+            }
+        }
+        __syncthreads();
+        int4* map = reinterpret_cast<int4*>(plan + plan_map_off(a.n_sess));
+        for (int pr = lane; pr < NT; pr += 64) {
+            const int ii = pr / NH, hh = pr - ii * NH;
+            const int x = s_home[ii];
+            const int rk = NH * s_rank[ii] + hh;
+            int t;
+            if (rk < s_cap[x]) {
+                t = x + 8 * rk;
+            } else {
+                const int o = s_ovpre[x] + (rk - s_cap[x]);
+                int x2 = 0;
+                for (int y = 0; y < 8; ++y) {
+                    const int fy = s_cap[y] > s_dem[y] ? s_cap[y] - s_dem[y] : 0;
+                    if (o >= s_freepre[y] && o < s_freepre[y] + fy) x2 = y;
+                }
+                t = x2 + 8 * (s_dem[x2] + (o - s_freepre[x2]));
+            }
+            map[t] = int4{s_kc[ii], s_k[ii], ii, hh};
+        }
         return;
     }
-    const Part pt = partition(a, w, -1);
-    int32_t* rec = plan + (int64_t)a.n_sess * 4 + (int64_t)w * kRec;
+    const Part pt = partition(a, logical_of(w, a.gw), -1);
+    int32_t* rec = plan + plan_rec_off(a.n_sess) + (int64_t)w * kRec;
     if (pt.sess < 0) {
         if (lane == 0) rec[kRecPages] = -1;
         return;
     }
-    const int j = w - pt.kc;
+    const int j = logical_of(w, a.gw) - pt.kc;
     const int pa = (int)((int64_t)j * pt.pages / pt.k);
     const int pb = (int)((int64_t)(j + 1) * pt.pages / pt.k);
     rec[lane] = pa + lane < pb ? a.tables[(int64_t)pt.sess * a.table_stride + pa + lane] : 0;
@@ -794,12 +864,12 @@ int batch_workgroups() {
 }
 
 void launch_pair(const DecodeArgs& a, int n_sess, float* o, hipStream_t st) {
-    const dim3 grid(a.gw + n_sess, a.kv_split ? NKV : 1);
+    const dim3 grid(a.plan ? split_slots(n_sess, a.gw) : a.gw + n_sess, a.kv_split ? NKV : 1);
     if (a.kv_split) hipLaunchKernelGGL((decode_split_kernel<false, true>), grid, dim3(THREADS), 0, st, a);
     else if (a.cs) hipLaunchKernelGGL((decode_split_kernel<true, false>), grid, dim3(THREADS), 0, st, a);
     else hipLaunchKernelGGL((decode_split_kernel<false, false>), grid, dim3(THREADS), 0, st, a);
     NOVA_LAUNCHED();
-    hipLaunchKernelGGL(decode_combine_kernel, dim3(n_sess, NH), dim3(CT), 0, st, a, o);
+    hipLaunchKernelGGL(decode_combine_kernel, dim3(n_sess * NH), dim3(CT), 0, st, a, o);
     NOVA_LAUNCHED();
 }
 
@@ -830,7 +900,7 @@ extern "C" {
 
 size_t attn_decode_batch_workspace_bytes(int n_sess) {
     NOVA_REQUIRE(n_sess >= 1 && n_sess <= kMaxBatch);
-    return plan_bytes(n_sess) + (size_t)(batch_workgroups() + n_sess) * R * NH * PW * sizeof(float);
+    return plan_bytes(n_sess) + (size_t)split_slots(n_sess, batch_workgroups()) * R * NH * PW * sizeof(float);
 }
 
 void launch_attn_decode_plan(const int32_t* tables, int table_stride, const int32_t* n_keys, int n_sess,
@@ -838,7 +908,7 @@ void launch_attn_decode_plan(const int32_t* tables, int table_stride, const int3
     NOVA_REQUIRE(n_keys);
     DecodeArgs a = batch_args(tables, table_stride, n_keys, n_sess, workspace);
     a.plan = nullptr;   // the plan kernel derives the partition itself
-    hipLaunchKernelGGL(decode_plan_kernel, dim3(a.gw + n_sess + 1), dim3(64), 0, reinterpret_cast<hipStream_t>(s),
+    hipLaunchKernelGGL(decode_plan_kernel, dim3(split_slots(n_sess, a.gw) + 1), dim3(64), 0, reinterpret_cast<hipStream_t>(s),
                        a, static_cast<int32_t*>(workspace));
     NOVA_LAUNCHED();
 }

@@ -107,6 +107,28 @@ def test_decode_batch_ragged_fused_append(model, oracle):
     print(f"  worst max|gpu-oracle|={worst:.3e}")
 
 
+def test_decode_batch_skewed_xcd_homes(nova7, oracle):
+    """One long session and 39 one-page sessions: the split workgroups fill
+    XCDs in logical order, so most sessions share two XCDs and their combine
+    blocks overflow onto the other XCDs' free blocks."""
+    nova = nova7
+    rng = np.random.default_rng(41)
+    n_keys = np.concatenate([[3000], rng.integers(1, 17, 39)]).astype(np.int32)
+    n_sess = len(n_keys)
+    max_pages = int((n_keys.max() + 15) // 16)
+    print(f"[case] decode batch skewed homes n_sess={n_sess}", flush=True)
+    fx = PagedFixture(nova, nb=n_sess * max_pages + 3, layer=LAYER, seed=41)
+    tables = fx.tables(n_sess, max_pages)
+    q = rng.standard_normal((n_sess, nova.nh, nova.hd)).astype(np.float32)
+    got = _batch(nova, fx, q, tables, n_keys)
+    worst = 0.0
+    for i in range(n_sess):
+        ref = oracle.attn_decode_paged("qwen25_7b", np.ascontiguousarray(q[i]), fx.hk, fx.hv, tables[i], 0,
+                                       fx.nb, int(n_keys[i]))
+        worst = max(worst, assert_close(got[i], ref, what=f"session {i} n_keys={n_keys[i]}"))
+    print(f"  worst max|gpu-oracle|={worst:.3e}")
+
+
 def test_decode_batch_empty_session_and_no_append(nova7, oracle):
     nova = nova7
     n_keys = np.array([40, 0, 1, 0, 300], np.int32)

@@ -116,19 +116,25 @@ struct DecodeArgs {
 // so a layer's split kernel starts with one load instead of a dependent
 // n_keys -> partition -> block-table chain.
 constexpr int kRecPages = 64;
-constexpr int kRec = kRecPages + 4;
+constexpr int kRec = kRecPages + 8;            // phys[64], {sess, pa, pb, n_keys, partial slot, 0, 0, 0}
 // Workgroup slots and XCDs.  Workgroup w runs on XCD w % 8.  The first
-// 8 * ceil(gw / 8) slots take the workgroups' logical indices XCD by XCD
-// (logical L = (w % 8) * per + w / 8), so a session's workgroups, which are
-// consecutive logical indices, share one or two XCDs and their partial rows
-// stay in those XCDs' L2 for the combine; slots past those map to themselves
-// (only used when the sessions outnumber what one round of gw workgroups can
-// split).
+// 8 * ceil(gw / 8) slots take the workgroups' logical indices XCD by XCD:
+// with S = sum k_i workgroups in the step and per = ceil(S / 8), slot w holds
+// logical L = (w % 8) * per + w / 8 (none if w / 8 >= per), so a session's
+// workgroups, which are consecutive logical indices, share one or two XCDs
+// and their partial rows stay in those XCDs' L2 for the combine, while a
+// small step still spreads over all 8 XCDs.  Slots past 8 ceil(gw / 8) map to
+// themselves (only used when the sessions outnumber what one round of gw
+// workgroups can split).
 __host__ __device__ constexpr int xcd_per(int gw) { return (gw + 7) / 8; }
 __host__ __device__ constexpr int split_slots(int n_sess, int gw) { return 8 * xcd_per(gw) + n_sess; }
-__host__ __device__ __forceinline__ int logical_of(int w, int gw) {
-    const int per = xcd_per(gw);
-    return w < 8 * per ? (w & 7) * per + (w >> 3) : w;
+__host__ __device__ __forceinline__ int xcd_stride(int sumk, int gw) {
+    const int per = (sumk + 7) / 8;
+    return per < 1 ? 1 : per < xcd_per(gw) ? per : xcd_per(gw);
+}
+__host__ __device__ __forceinline__ int logical_of(int w, int stride, int gw) {
+    if (w >= 8 * xcd_per(gw)) return w;
+    return (w >> 3) < stride ? (w & 7) * stride + (w >> 3) : -1;
 }
 // plan: [session table n_sess x 4 | combine map n_sess*NH x 4 | records]
 __host__ __device__ constexpr int64_t plan_map_off(int n_sess) { return (int64_t)n_sess * 4; }
@@ -253,6 +259,33 @@ __device__ Part partition(const DecodeArgs& a, int w, int want) {
     return r;
 }
 
+// Workgroups of the batch, sum of k_i (one wave).
+__device__ int sum_k(const DecodeArgs& a) {
+    const int lane = threadIdx.x & 63;
+    int T = 0;
+    for (int base = 0; base < a.n_sess; base += 64) {
+        const int i = base + lane;
+        const int nk = i < a.n_sess ? nkeys_of(a, i) : 0;
+        int pg = nk > 0 ? (nk + kKvBlock - 1) >> kKvBlockShift : 0;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) pg += __shfl_xor(pg, o, 64);
+        T += pg;
+    }
+    if (T == 0) return 0;
+    const int target = plan_share(a, T);
+    int sumk = 0;
+    for (int base = 0; base < a.n_sess; base += 64) {
+        const int i = base + lane;
+        const int nk = i < a.n_sess ? nkeys_of(a, i) : 0;
+        const int pg = nk > 0 ? (nk + kKvBlock - 1) >> kKvBlockShift : 0;
+        int k = (pg + target - 1) / target;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) k += __shfl_xor(k, o, 64);
+        sumk += k;
+    }
+    return sumk;
+}
+
 // K and V operands of one pair of pages, as loaded
 struct PairRegs {
     u4 k0[4], k1[4];   // K of page 0 / page 1 as whole-line loads (k_operand)
@@ -300,17 +333,18 @@ decode_split_kernel(DecodeArgs a) {
     constexpr int RS = kKvSplit ? WAVES : R;        // waves per kv head = pair stride
     const int w = blockIdx.x;
 
-    int i, n_keys, pa, pb, tv;
+    int i, n_keys, pa, pb, tv, slot = w;        // slot: this workgroup's partial row index
     if (a.plan) {
         // one load: lane t holds phys[t]; lanes 0..3 the header
         const int32_t* rec = a.plan + plan_rec_off(a.n_sess) + (int64_t)w * kRec;
         tv = rec[lane];
-        const int hv = rec[kRecPages + (lane & 3)];
+        const int hv = rec[kRecPages + (lane & 7)];
         i = __builtin_amdgcn_readlane(hv, 0);
         if (i < 0) return;                       // idle workgroup (uniform)
         pa = __builtin_amdgcn_readlane(hv, 1);
         pb = __builtin_amdgcn_readlane(hv, 2);
         n_keys = __builtin_amdgcn_readlane(hv, 3);
+        slot = __builtin_amdgcn_readlane(hv, 4);
     } else {
         const Part pt = partition(a, w, -1);
         if (pt.sess < 0) return;                 // idle workgroup (uniform)
@@ -590,10 +624,10 @@ decode_split_kernel(DecodeArgs a) {
             }
         };
         if constexpr (R == 1 && !kKvSplit) {
-            write_rows(a.part + (int64_t)(a.plan ? logical_of(w, a.gw) : w) * NH * PW);
+            write_rows(a.part + (int64_t)slot * NH * PW);
         } else if (a.wave_parts) {
             // slot w*R + r: the combine merges the R rows with the workgroups'
-            write_rows(a.part + ((int64_t)(a.plan ? logical_of(w, a.gw) : w) * R + r) * NH * PW);
+            write_rows(a.part + ((int64_t)slot * R + r) * NH * PW);
         } else {
             // merge the waves of each kv head in LDS (kv-split: the G heads of
             // this workgroup's kv head over all its waves)
@@ -749,7 +783,7 @@ decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
     const int w = blockIdx.x, lane = threadIdx.x;
     const int n_slots = split_slots(a.n_sess, a.gw);
     if (w == n_slots) {
-        __shared__ int s_kc[kMaxBatch], s_k[kMaxBatch], s_home[kMaxBatch], s_rank[kMaxBatch];
+        __shared__ int s_kc[kMaxBatch], s_k[kMaxBatch], s_mid[kMaxBatch], s_home[kMaxBatch], s_rank[kMaxBatch];
         // session table: the same prefix as partition(), one lane per session
         int T = 0;
         for (int base = 0; base < a.n_sess; base += 64) {
@@ -782,10 +816,7 @@ decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
                 e[3] = pg;
                 s_kc[ii] = kc;
                 s_k[ii] = k;
-                // home XCD: the one that runs the session's middle workgroup
-                const int per = xcd_per(a.gw);
-                const int mid = kc + (k > 0 ? (k - 1) / 2 : 0);
-                s_home[ii] = mid < 8 * per ? mid / per : 0;
+                s_mid[ii] = kc + (k > 0 ? (k - 1) / 2 : 0);
             }
             carry += __shfl(incl, 63, 64);
         }
@@ -793,6 +824,13 @@ decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
         // (session, head) pairs of its own sessions, the overflow fills the
         // blocks other XCDs leave free
         __shared__ int s_cap[8], s_dem[8], s_ovpre[8], s_freepre[8];
+        __syncthreads();
+        // home XCD: the one that runs the session's middle workgroup
+        {
+            const int stride = xcd_stride(carry, a.gw);
+            for (int ii = lane; ii < a.n_sess; ii += 64)
+                s_home[ii] = s_mid[ii] < 8 * stride ? s_mid[ii] / stride : 0;
+        }
         __syncthreads();
         const int NT = a.n_sess * NH;
         if (lane == 0) {
@@ -832,18 +870,19 @@ decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
         }
         return;
     }
-    const Part pt = partition(a, logical_of(w, a.gw), -1);
+    const int L = logical_of(w, xcd_stride(sum_k(a), a.gw), a.gw);
+    const Part pt = L >= 0 ? partition(a, L, -1) : Part{-1, 0, 0, 0, 0};
     int32_t* rec = plan + plan_rec_off(a.n_sess) + (int64_t)w * kRec;
     if (pt.sess < 0) {
         if (lane == 0) rec[kRecPages] = -1;
         return;
     }
-    const int j = logical_of(w, a.gw) - pt.kc;
+    const int j = L - pt.kc;
     const int pa = (int)((int64_t)j * pt.pages / pt.k);
     const int pb = (int)((int64_t)(j + 1) * pt.pages / pt.k);
     rec[lane] = pa + lane < pb ? a.tables[(int64_t)pt.sess * a.table_stride + pa + lane] : 0;
-    if (lane < 4) {
-        const int v = lane == 0 ? pt.sess : lane == 1 ? pa : lane == 2 ? pb : pt.n_keys;
+    if (lane < 5) {
+        const int v = lane == 0 ? pt.sess : lane == 1 ? pa : lane == 2 ? pb : lane == 3 ? pt.n_keys : L;
         rec[kRecPages + lane] = v;
     }
 }

@@ -78,8 +78,10 @@ size_t attn_decode_batch_workspace_bytes(int n_sess);
 /* The batched call above = launch_attn_decode_plan + launch_attn_decode_paged_planned.
  * A decode step has the same n_keys and block tables in every layer, so a
  * caller can plan once per step and run only the planned call per layer:
- * the plan records each workgroup's session, page range and physical pages,
- * and the planned call starts from one load instead of a dependent
+ * the plan records each workgroup's session, page range, physical pages and
+ * partial slot (a session's workgroups are grouped on one or two XCDs) and
+ * the (session, head) each combine block merges (on its session's XCD where
+ * there is room), and the planned call starts from one load instead of a dependent
  * n_keys -> partition -> block-table chain.  The plan lives at the start of
  * `workspace`; it is valid until n_keys or the tables change. */
 void launch_attn_decode_plan(const int32_t* tables, int table_stride, const int32_t* n_keys, int n_sess,

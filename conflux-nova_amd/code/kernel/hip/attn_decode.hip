@@ -328,10 +328,13 @@ decode_split_kernel(DecodeArgs a) {
     const int c = lane & 15;      // 0..15
     // kv-split: workgroup (w, kv head) streams that head's rows of its page
     // range with all waves; otherwise wave w serves kv head w % NKV
-    const int kvh = kKvSplit ? (int)blockIdx.y : wave % NKV;
+    // kv-split grid is (NKV, ranges): block id kvh + NKV * range runs on XCD
+    // (kvh + NKV * range) % 8, so one kv head's workgroups share the XCDs
+    // congruent to kvh mod NKV, where its combine blocks run too
+    const int kvh = kKvSplit ? (int)blockIdx.x : wave % NKV;
     const int r = kKvSplit ? wave : wave / NKV;
     constexpr int RS = kKvSplit ? WAVES : R;        // waves per kv head = pair stride
-    const int w = blockIdx.x;
+    const int w = kKvSplit ? (int)blockIdx.y : (int)blockIdx.x;
 
     int i, n_keys, pa, pb, tv, slot = w;        // slot: this workgroup's partial row index
     if (a.plan) {
@@ -688,6 +691,7 @@ decode_split_kernel(DecodeArgs a) {
 // results are merged through LDS by the same rule.  Measured against one
 // workgroup per (session, kv head) walking all slots: 448 instead of 64
 // workgroups for config 2, 0.876 -> 0.859 ms per step.
+static_assert(8 % NKV == 0, "kv heads must divide the 8 XCDs");
 constexpr int CT = 256;                       // combine threads
 constexpr int kCombGroups = CT / (HD / 4);
 
@@ -708,8 +712,19 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
         h = e.w;
         pt.sess = i;
     } else {
-        i = t % a.n_sess;
-        h = t / a.n_sess;
+        if (a.kv_split) {
+            // single session: head kvh * G + m runs on a block whose XCD
+            // (t % 8) is congruent to kvh mod NKV, next to its split workgroups
+            constexpr int per8 = 8 / NKV;
+            const int x = t & 7, kv = x % NKV;
+            const int m = (t >> 3) * per8 + x / NKV;
+            if (m >= G) return;                  // padding block
+            i = 0;
+            h = kv * G + m;
+        } else {
+            i = t % a.n_sess;
+            h = t / a.n_sess;
+        }
         pt = partition(a, 0, i);
     }
     f4* orow = reinterpret_cast<f4*>(o + ((int64_t)i * NH + h) * HD) + q4;
@@ -903,12 +918,14 @@ int batch_workgroups() {
 }
 
 void launch_pair(const DecodeArgs& a, int n_sess, float* o, hipStream_t st) {
-    const dim3 grid(a.plan ? split_slots(n_sess, a.gw) : a.gw + n_sess, a.kv_split ? NKV : 1);
+    const dim3 grid = a.kv_split ? dim3(NKV, a.gw + n_sess)
+                                 : dim3(a.plan ? split_slots(n_sess, a.gw) : a.gw + n_sess);
     if (a.kv_split) hipLaunchKernelGGL((decode_split_kernel<false, true>), grid, dim3(THREADS), 0, st, a);
     else if (a.cs) hipLaunchKernelGGL((decode_split_kernel<true, false>), grid, dim3(THREADS), 0, st, a);
     else hipLaunchKernelGGL((decode_split_kernel<false, false>), grid, dim3(THREADS), 0, st, a);
     NOVA_LAUNCHED();
-    hipLaunchKernelGGL(decode_combine_kernel, dim3(n_sess * NH), dim3(CT), 0, st, a, o);
+    const int comb = a.plan ? n_sess * NH : a.kv_split ? 8 * ((NH + 7) / 8) : n_sess * NH;
+    hipLaunchKernelGGL(decode_combine_kernel, dim3(comb), dim3(CT), 0, st, a, o);
     NOVA_LAUNCHED();
 }
 

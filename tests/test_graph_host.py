@@ -13,6 +13,13 @@ from pool_replay import load_traces, replay, replay_fork, replay_probe
 GOLDEN = Path(__file__).resolve().parent / "golden"
 
 
+@pytest.fixture(autouse=True, params=["host", pytest.param("gpu_box", marks=pytest.mark.gpu)])
+def where(request):
+    """every test here runs in the CPU suite and again, marked gpu, in the GPU
+    box's run, so the product's host paging layer is part of that record"""
+    return request.param
+
+
 @pytest.fixture(scope="module")
 def prod_pool(nova7):
     from oracle_py import PoolAPI

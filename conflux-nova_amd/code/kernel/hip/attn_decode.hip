@@ -947,6 +947,40 @@ DecodeArgs batch_args(const int32_t* tables, int table_stride, const int32_t* n_
     return a;
 }
 
+// ---- workspace without allocation: a file-scope device array ----
+// For callers that cannot allocate (code under graph capture, serving loops,
+// harnesses that forbid hipMalloc): the batched decode with its plan and
+// partials in this array instead of a caller workspace.  Sized for
+// kStaticMaxSess sessions on a device of at most kStaticMaxCUs CUs.  Each
+// device holds its own copy for the life of the process; every call on a
+// device shares it, so calls that overlap on one device race.  Nothing in it
+// needs initial contents: the plan kernel writes every record and combine-map
+// entry it later reads, and the split kernel writes every partial row.
+constexpr int kStaticMaxSess = 64;
+constexpr int kStaticMaxCUs = 256;
+constexpr size_t kStaticPlanBytes = ((size_t)plan_ints(kStaticMaxSess, kStaticMaxCUs) * 4 + 255) / 256 * 256;
+constexpr size_t kStaticBytes =
+    kStaticPlanBytes + (size_t)split_slots(kStaticMaxSess, kStaticMaxCUs) * R * NH * PW * sizeof(float);
+__device__ __align__(256) unsigned char scratch[kStaticBytes];
+
+// Device address of `scratch` on the current device, looked up once per device
+// with that device current (the host-side name is only a stand-in).
+void* scratch_address() {
+    constexpr int kMaxDevices = 64;
+    static void* ptr[kMaxDevices] = {};
+    static std::once_flag once[kMaxDevices];
+    int dev = 0;
+    NOVA_HIP(hipGetDevice(&dev));
+    NOVA_REQUIRE(dev >= 0 && dev < kMaxDevices);
+    std::call_once(once[dev], [dev] {
+        void* p = nullptr;
+        NOVA_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        NOVA_REQUIRE(p != nullptr);
+        ptr[dev] = p;
+    });
+    return ptr[dev];
+}
+
 }  // namespace
 }  // namespace nova
 
@@ -1022,6 +1056,29 @@ void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* 
     launch_attn_decode_plan(tables, table_stride, n_keys, n_sess, workspace, s);
     launch_attn_decode_paged_planned(q, pool_k, pool_v, tables, table_stride, n_sess, layer, nb, k_new, v_new, o,
                                      workspace, s);
+}
+
+void launch_attn_decode_paged_batch_noalloc(const float* q, uint16_t* pool_k, uint16_t* pool_v,
+                                            const int32_t* tables, int table_stride, const int32_t* n_keys,
+                                            int n_sess, int layer, int nb, const uint16_t* k_new,
+                                            const uint16_t* v_new, float* o, nova_stream_t s) {
+    // checked on the host before anything is launched (sessions first: no HIP call)
+    const int cus = (n_sess >= 1 && n_sess <= kStaticMaxSess) ? batch_workgroups() : 0;
+    if (cus < 1 || cus > kStaticMaxCUs) {
+        std::fflush(stdout);
+        std::fprintf(stderr,
+                     "[nova] FATAL launch_attn_decode_paged_batch_noalloc: the static workspace (%zu bytes) "
+                     "covers 1..%d sessions on at most %d CUs; called with n_sess %d%s. Use "
+                     "launch_attn_decode_paged_batch with a workspace instead.\n",
+                     kStaticBytes, kStaticMaxSess, kStaticMaxCUs, n_sess, cus > kStaticMaxCUs ? " on a larger device" : "");
+        std::fflush(stderr);
+        std::abort();
+    }
+    NOVA_REQUIRE(attn_decode_batch_workspace_bytes(n_sess) <= kStaticBytes);
+    void* ws = scratch_address();
+    launch_attn_decode_plan(tables, table_stride, n_keys, n_sess, ws, s);
+    launch_attn_decode_paged_planned(q, pool_k, pool_v, tables, table_stride, n_sess, layer, nb, k_new, v_new, o,
+                                     ws, s);
 }
 
 void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint16_t* pool_v,

@@ -94,6 +94,20 @@ void launch_attn_decode_paged_batch(const float* q, uint16_t* pool_k, uint16_t* 
                                     int n_sess, int layer, int nb,
                                     const uint16_t* k_new, const uint16_t* v_new,
                                     float* o, void* workspace, nova_stream_t s);
+/* The batched decode above (plan + split + combine) with no workspace
+ * argument and no allocation: the plan and partials live in a static device
+ * array inside the library (about 10 MB per device, held until the process
+ * ends).  No counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Limits: n_sess <= 64 on a device of at most 256
+ * CUs; anything else aborts with a message before launching.  Every call on
+ * a device shares the array, so calls that overlap on one device (two
+ * streams) race; calls in one stream order are safe.  Nothing in the array
+ * needs clearing between calls. */
+void launch_attn_decode_paged_batch_noalloc(const float* q, uint16_t* pool_k, uint16_t* pool_v,
+                                            const int32_t* tables, int table_stride, const int32_t* n_keys,
+                                            int n_sess, int layer, int nb, const uint16_t* k_new,
+                                            const uint16_t* v_new, float* o, nova_stream_t s);
 /* The batched decode with the step before it fused in: RopeKvOp
  * (code/graph/dense.h:75-83: rope_batch of q and k at position n_keys[i]-1,
  * src/kernel/rope.cu:21-58, then kv_store_paged of k and v) and the

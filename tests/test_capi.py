@@ -95,3 +95,13 @@ def test_bad_arguments_abort_before_launch(call, needle):
     r = _abort_run(f"import nova_amd; n = nova_amd.load('qwen25_7b'); {call}")
     assert r.returncode != 0
     assert "requirement failed" in r.stderr and needle in r.stderr, r.stderr[-500:]
+
+
+@pytest.mark.parametrize("n_sess", [0, 65])
+def test_noalloc_decode_rejects_sizes_beyond_its_workspace(n_sess):
+    """the allocation-free batched decode refuses session counts its static
+    workspace does not cover, on the host, before any HIP call"""
+    r = _abort_run("import nova_amd; n = nova_amd.load('qwen25_7b'); "
+                   f"n.launch_attn_decode_paged_batch_noalloc(1, 1, 1, 1, 4, 1, {n_sess}, 0, 4, None, None, 1, None)")
+    assert r.returncode != 0
+    assert "static workspace" in r.stderr and f"n_sess {n_sess}" in r.stderr, r.stderr[-500:]

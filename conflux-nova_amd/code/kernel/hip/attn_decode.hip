@@ -58,6 +58,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 
 #include "check.h"
 #include "model.h"
@@ -159,6 +160,14 @@ __device__ __forceinline__ u4 ld16(const char* base, uint32_t off) {
 __device__ __forceinline__ u4 ld16_nt(const char* base, uint32_t off) {
     return __builtin_nontemporal_load(reinterpret_cast<const u4*>(base + off));
 }
+
+#ifdef NOVA_DECODE_TRACE
+// per-workgroup timeline (development builds only): 8 x 64-bit per workgroup slot
+__device__ uint64_t g_trace[2048 * 8];
+#define TRACE(k) do { if ((threadIdx.x & 63) == 0) g_trace[(int64_t)blockIdx.x * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define TRACE(k) do {} while (0)
+#endif
 
 // Pages per workgroup: the even share ceil(T / gw), but at least kMinShare so
 // that small batches do not spread one or two pages per workgroup (each extra
@@ -335,6 +344,7 @@ decode_split_kernel(DecodeArgs a) {
     const int r = kKvSplit ? wave : wave / NKV;
     constexpr int RS = kKvSplit ? WAVES : R;        // waves per kv head = pair stride
     const int w = kKvSplit ? (int)blockIdx.y : (int)blockIdx.x;
+    if (wave == 0) TRACE(0);
 
     int i, n_keys, pa, pb, tv, slot = w;        // slot: this workgroup's partial row index
     if (a.plan) {
@@ -358,6 +368,10 @@ decode_split_kernel(DecodeArgs a) {
         pb = (int)((int64_t)(j + 1) * pt.pages / pt.k);
         tv = (pa + lane < pb) ? a.tables[(int64_t)i * a.table_stride + pa + lane] : 0;
     }
+    // settle the slice register here (one wait, nothing else in flight yet):
+    // otherwise the compiler's wait before its first read, after the query and
+    // first-pair loads below are issued, would be a wait for all of them
+    asm volatile("v_mov_b32 %0, %1" : "=v"(tv) : "v"(tv));
     const int last_page = (n_keys - 1) >> kKvBlockShift;
     const int32_t* table = a.tables + (int64_t)i * a.table_stride;
 
@@ -385,11 +399,17 @@ decode_split_kernel(DecodeArgs a) {
         };
 
         const int npairs = (pb - pa + 1) >> 1;
-        auto load_pair = [&](int qp, PairRegs& pr) {
+        // kFirst: a wave's first pair (pages < 16 into the range) takes its pages
+        // straight from the slice register, with no reload branch: a reload's
+        // load would make the first pair's issue wait for every load before it
+        auto load_pair = [&](auto first_tag, int qp, PairRegs& pr) {
+            constexpr bool kFirst = decltype(first_tag)::value;
             const int pg0 = pa + 2 * qp;
             const int pg1 = pg0 + 1 < pb ? pg0 + 1 : pg0;   // a lone last page loads itself twice
-            const int64_t b0 = (layer_page0 + phys_of(pg0)) * kPageBytes;
-            const int64_t b1 = (layer_page0 + phys_of(pg1)) * kPageBytes;
+            const int ph0 = kFirst ? __builtin_amdgcn_readlane(tv, pg0 - pa) : phys_of(pg0);
+            const int ph1 = kFirst ? __builtin_amdgcn_readlane(tv, pg1 - pa) : phys_of(pg1);
+            const int64_t b0 = (layer_page0 + ph0) * kPageBytes;
+            const int64_t b1 = (layer_page0 + ph1) * kPageBytes;
             const char* k0 = pk + b0;
             const char* k1 = pk + b1;
             const char* v0 = pv + b0;
@@ -407,17 +427,51 @@ decode_split_kernel(DecodeArgs a) {
             }
         };
 
-        // The first pair's loads go out now, together with the Q loads below,
-        // unless the fused append is about to write into it (then after the barrier).
+        // Issue order: the appended token's row and the query rows first, then
+        // the first pair (unless the fused append is about to write into it:
+        // then after the barrier).  The vector-memory counter drains in issue
+        // order, so waiting for the query or the token row waits only for what
+        // was issued before it -- issued after the pair, the query conversion
+        // (and the barrier behind it) would wait for the whole pair to arrive.
         const bool appends = (kRope || a.k_new) && pb == last_page + 1;
         const bool early = !(appends && pa + 2 * r + 1 >= last_page);
+        // Every wave issues the same loads in the same order, whatever its
+        // role, so that the compiler's waits count exactly: a wave without a
+        // use for one reads a valid line and drops it.
+        const int phys_last = table[last_page];     // the appended token's page (may lie past the slice register)
+        static_assert(KVW / 8 <= THREADS, "one 16-byte piece of the appended row per thread");
+        const bool app_thread = !kRope && appends && tid < KVW / 8;
+        u4 knew, vnew;
+        {
+            const uint16_t* ks = a.k_new ? a.k_new : reinterpret_cast<const uint16_t*>(a.q);
+            const uint16_t* vs = a.v_new ? a.v_new : reinterpret_cast<const uint16_t*>(a.q);
+            const int64_t src = app_thread ? (int64_t)i * KVW + 8 * tid : 0;
+            knew = *reinterpret_cast<const u4*>(ks + src);
+            vnew = *reinterpret_cast<const u4*>(vs + src);
+        }
+        f4 qraw[8];
+        const bool qreal = c < G;
+        {
+            // the converting wave of each kv head (r == 0) reads its rows; the others one line
+            const int64_t qoff = r == 0 ? ((int64_t)i * NH + kvh * G + (qreal ? c : 0)) * HD + 8 * g : (int64_t)i * NH * HD;
+            const int step = r == 0 ? 1 : 0;
+            const float* qp = a.q + qoff;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                qraw[2 * ks] = *reinterpret_cast<const f4*>(qp + step * (32 * ks));
+                qraw[2 * ks + 1] = *reinterpret_cast<const f4*>(qp + step * (32 * ks + 4));
+            }
+        }
         PairRegs cur;
-        if (r < npairs && early) load_pair(r, cur);
+        static_assert(2 * (8 - 1) + 1 < 64, "a first pair lies in the slice register");
+        // the first pair (a wave without one, or whose pair the append is about
+        // to write, loads page pa's pair and reloads after the barrier)
+        load_pair(std::true_type{}, (r < npairs && early) ? r : 0, cur);
 
         // fused append: the owner of the session's last page stores the new
         // token; the barrier below publishes it to the waves of this workgroup
         if (appends) {
-            const int phys = table[last_page];
+            const int phys = phys_last;
             const int64_t dst = ((layer_page0 + phys) * kPageBytes + (int64_t)((n_keys - 1) & kKvBlockMask) * kRowBytes) / 2;
             const int64_t src = (int64_t)i * KVW;
             if constexpr (kRope) {
@@ -437,13 +491,10 @@ decode_split_kernel(DecodeArgs a) {
                 }
                 for (int e = tid; e < KVW; e += THREADS)
                     pv16[e] = __builtin_bit_cast(uint16_t, (_Float16)a.v_new32[src + e]);
-            } else {
-                for (int e = tid; e < KVW / 8; e += THREADS) {
-                    *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_k) + dst + 8 * e) =
-                        *reinterpret_cast<const u4*>(a.k_new + src + 8 * e);
-                    *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_v) + dst + 8 * e) =
-                        *reinterpret_cast<const u4*>(a.v_new + src + 8 * e);
-                }
+            } else if (app_thread) {
+                (void)src;
+                *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_k) + dst + 8 * tid) = knew;
+                *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_v) + dst + 8 * tid) = vnew;
             }
         }
 
@@ -453,16 +504,12 @@ decode_split_kernel(DecodeArgs a) {
         if (r == 0) {
             float qv[4][8];
             float amax = 0.f;
-            const bool real = c < G;
-            const float* qp = a.q + ((int64_t)i * NH + kvh * G + (real ? c : 0)) * HD + 8 * g;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const f4 x0 = *reinterpret_cast<const f4*>(qp + 32 * ks);
-                const f4 x1 = *reinterpret_cast<const f4*>(qp + 32 * ks + 4);
 #pragma unroll
                 for (int jj = 0; jj < 4; ++jj) {
-                    qv[ks][jj] = real ? x0[jj] : 0.f;
-                    qv[ks][4 + jj] = real ? x1[jj] : 0.f;
+                    qv[ks][jj] = qreal ? qraw[2 * ks][jj] : 0.f;
+                    qv[ks][4 + jj] = qreal ? qraw[2 * ks + 1][jj] : 0.f;
                 }
             }
             if constexpr (kRope) {
@@ -509,6 +556,7 @@ decode_split_kernel(DecodeArgs a) {
             }
         }
         __syncthreads();
+        if (wave == 0) TRACE(1);
         const float qf = s_qf[kvh][c];
 
         float m = -INFINITY, lsum = 0.f;
@@ -592,12 +640,15 @@ decode_split_kernel(DecodeArgs a) {
         };
 
         // each wave keeps one pair (16 KiB) in flight; the 8 waves of the CU
-        // overlap each other's latency (measured: a register ping-pong of two
-        // pairs per wave, with Q re-read from LDS to fit 256 VGPRs, is slower)
+        // overlap each other's latency (measured: a second pair prefetched
+        // before the query conversion only delays the query rows further
+        // behind the chip's first burst, 0.778 -> 0.791 ms per config-2 step)
         for (int qp = r; qp < npairs; qp += RS) {
-            if (qp != r || !early) load_pair(qp, cur);
+            if (qp != r || !early) load_pair(std::false_type{}, qp, cur);
             compute_pair(qp, cur);
+            if (wave == 0 && qp == r) TRACE(2);
         }
+        if (wave == 0) TRACE(3);
 
         lsum += shfl_xor_f(lsum, 16);
         lsum += shfl_xor_f(lsum, 32);
@@ -628,6 +679,81 @@ decode_split_kernel(DecodeArgs a) {
         };
         if constexpr (R == 1 && !kKvSplit) {
             write_rows(a.part + (int64_t)slot * NH * PW);
+        } else if (a.wave_parts == 2 && !kKvSplit) {
+            // one partial slot per workgroup: the R waves of a kv head merge
+            // through LDS with no serial pass.  Lane group g (head dims
+            // [32g, 32g + 32)) of wave r keeps its dims when g*R/4 == r and
+            // hands them to that wave otherwise; each keeper merges the R rows
+            // of its 32 dims by the combine rule and stores them.
+            const int keeper = (g * R) >> 2;
+            if (g == 0) {
+                s_m[wave][c] = m;
+                s_l[wave][c] = lsum;
+            }
+            if (keeper != r && c < G) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    f4 lo4, hi4;
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) {
+                        lo4[cb] = acc[cb][ii];
+                        hi4[cb] = acc[cb + 4][ii];
+                    }
+                    *reinterpret_cast<f4*>(&s_acc[wave][c][8 * (4 * g + ii)]) = lo4;
+                    *reinterpret_cast<f4*>(&s_acc[wave][c][8 * (4 * g + ii) + 4]) = hi4;
+                }
+            }
+            __syncthreads();
+            if (keeper == r && c < G) {
+                float M = -INFINITY;
+#pragma unroll
+                for (int rr = 0; rr < R; ++rr) {
+                    const int ww = kvh + NKV * rr;
+                    if (s_l[ww][c] > 0.f) M = fmaxf(M, s_m[ww][c]);
+                }
+                float L = 0.f;
+                f4 A[8];
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb) A[cb] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int rr = 0; rr < R; ++rr) {
+                    const int ww = kvh + NKV * rr;
+                    const float lw = s_l[ww][c];
+                    const float f = lw > 0.f ? exp2f(s_m[ww][c] - M) : 0.f;
+                    L = fmaf(lw, f, L);
+                    if (rr == r) {
+#pragma unroll
+                        for (int cb = 0; cb < 8; ++cb) A[cb] += acc[cb] * f;
+                    } else {
+#pragma unroll
+                        for (int ii = 0; ii < 4; ++ii) {
+                            const f4 lo4 = *reinterpret_cast<const f4*>(&s_acc[ww][c][8 * (4 * g + ii)]);
+                            const f4 hi4 = *reinterpret_cast<const f4*>(&s_acc[ww][c][8 * (4 * g + ii) + 4]);
+#pragma unroll
+                            for (int cb = 0; cb < 4; ++cb) {
+                                A[cb][ii] = fmaf(lo4[cb], f, A[cb][ii]);
+                                A[cb + 4][ii] = fmaf(hi4[cb], f, A[cb + 4][ii]);
+                            }
+                        }
+                    }
+                }
+                float* row = a.part + ((int64_t)slot * NH + kvh * G + c) * PW;
+                if (g == 0) {
+                    row[0] = M;
+                    row[1] = L;
+                }
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) {
+                    f4 lo4, hi4;
+#pragma unroll
+                    for (int cb = 0; cb < 4; ++cb) {
+                        lo4[cb] = A[cb][ii];
+                        hi4[cb] = A[cb + 4][ii];
+                    }
+                    *reinterpret_cast<f4*>(row + 2 + 8 * (4 * g + ii)) = lo4;
+                    *reinterpret_cast<f4*>(row + 2 + 8 * (4 * g + ii) + 4) = hi4;
+                }
+            }
         } else if (a.wave_parts) {
             // slot w*R + r: the combine merges the R rows with the workgroups'
             write_rows(a.part + ((int64_t)slot * R + r) * NH * PW);
@@ -680,6 +806,10 @@ decode_split_kernel(DecodeArgs a) {
             }
         }
     }
+#ifdef NOVA_DECODE_TRACE
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (wave == 0) TRACE(4);
+#endif
 }
 
 // Combine: one workgroup per (session, head) merges the session's k_i
@@ -734,7 +864,7 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     }
     constexpr int64_t SEG = (int64_t)NH * PW;
     constexpr int kChunk = 8;
-    const int rows = a.wave_parts ? R : 1;         // partial slots per split workgroup
+    const int rows = a.wave_parts == 1 ? R : 1;    // partial slots per split workgroup
     pt.kc *= rows;
     pt.k *= rows;
     const float* base = a.part + (int64_t)pt.kc * SEG + (int64_t)h * PW;
@@ -917,13 +1047,17 @@ int batch_workgroups() {
     return gw;
 }
 
-void launch_pair(const DecodeArgs& a, int n_sess, float* o, hipStream_t st) {
+void launch_split(const DecodeArgs& a, int n_sess, hipStream_t st) {
     const dim3 grid = a.kv_split ? dim3(NKV, a.gw + n_sess)
                                  : dim3(a.plan ? split_slots(n_sess, a.gw) : a.gw + n_sess);
     if (a.kv_split) hipLaunchKernelGGL((decode_split_kernel<false, true>), grid, dim3(THREADS), 0, st, a);
     else if (a.cs) hipLaunchKernelGGL((decode_split_kernel<true, false>), grid, dim3(THREADS), 0, st, a);
     else hipLaunchKernelGGL((decode_split_kernel<false, false>), grid, dim3(THREADS), 0, st, a);
     NOVA_LAUNCHED();
+}
+
+void launch_pair(const DecodeArgs& a, int n_sess, float* o, hipStream_t st) {
+    launch_split(a, n_sess, st);
     const int comb = a.plan ? n_sess * NH : a.kv_split ? 8 * ((NH + 7) / 8) : n_sess * NH;
     hipLaunchKernelGGL(decode_combine_kernel, dim3(comb), dim3(CT), 0, st, a, o);
     NOVA_LAUNCHED();
@@ -943,7 +1077,10 @@ DecodeArgs batch_args(const int32_t* tables, int table_stride, const int32_t* n_
     a.gw = batch_workgroups();
     a.plan = static_cast<const int32_t*>(workspace);
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan_bytes(n_sess));
-    a.wave_parts = 1;
+#ifndef NOVA_DECODE_PART_MODE
+#define NOVA_DECODE_PART_MODE 2
+#endif
+    a.wave_parts = R > 1 ? NOVA_DECODE_PART_MODE : 1;
     return a;
 }
 
@@ -988,6 +1125,10 @@ using namespace nova;
 
 extern "C" {
 
+#ifdef NOVA_DECODE_TRACE
+void nova_decode_trace_copy(void* host) { NOVA_HIP(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), sizeof(g_trace))); }
+#endif
+
 size_t attn_decode_batch_workspace_bytes(int n_sess) {
     NOVA_REQUIRE(n_sess >= 1 && n_sess <= kMaxBatch);
     return plan_bytes(n_sess) + (size_t)split_slots(n_sess, batch_workgroups()) * R * NH * PW * sizeof(float);
@@ -1018,6 +1159,23 @@ void launch_attn_decode_paged_planned(const float* q, uint16_t* pool_k, uint16_t
     a.k_new = k_new;
     a.v_new = v_new;
     launch_pair(a, n_sess, o, reinterpret_cast<hipStream_t>(s));
+}
+
+void testkit_attn_decode_split_only(const float* q, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
+                                    int table_stride, int n_sess, int layer, int nb, const uint16_t* k_new,
+                                    const uint16_t* v_new, void* workspace, nova_stream_t s) {
+    NOVA_REQUIRE(q && pool_k && pool_v);
+    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0);
+    NOVA_REQUIRE((k_new == nullptr) == (v_new == nullptr));
+    DecodeArgs a = batch_args(tables, table_stride, nullptr, n_sess, workspace);
+    a.q = q;
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.layer = layer;
+    a.nb = nb;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    launch_split(a, n_sess, reinterpret_cast<hipStream_t>(s));
 }
 
 void launch_attn_decode_paged_rope_planned(const float* q, const float* k_new, const float* v_new, const float* cs,

@@ -41,18 +41,20 @@
 //  * Rows past the workgroup's last key (unwritten slots may hold NaN bits)
 //    are loaded from the last key's row instead, so masked weights never
 //    meet NaN operands.
-//  * Q is converted to fp16 once (scaled by 1/sqrt(HD)*log2 e); P is fp16;
-//    accumulation is fp32.  The row sums l come from the matrix core too
+//  * Q (scaled by 1/sqrt(HD)*log2 e and a per-column power of two) is split
+//    once into hi + lo fp16 terms, each with its own score MFMA, so scores
+//    carry ~2^-22 relative error per operand instead of fp16's 2^-11 (real
+//    post-RoPE queries are far from unit scale); P is fp16; accumulation is
+//    fp32.  The row sums l come from the matrix core too
 //    (one MFMA of an all-ones operand with P^T per block), so they are the
 //    sums of exactly the fp16 weights applied to V, at no VALU cost.
 //  * Lazy rescaling: a column's running max m only moves when a tile's max
 //    exceeds it by more than 8 (log2 units), bounding P by 2^8 in fp16, so the
-//    O rescale (32 multiplies per block) is skipped on most tiles.  The score
-//    MFMAs start from -m (accumulator seed), so they yield s - m directly; the
+//    O rescale (32 multiplies per block) is skipped on most tiles.  Each score
+//    becomes s - m in one fma (undoing the column's power-of-two scale); the
 //    common case is one lane-local comparison against 8 and a wave ballot,
 //    and only a rescale takes the row max across the four 16-lane rows
-//    (v_permlane16/32_swap, no LDS round trip) and corrects the next tile's
-//    already-issued scores by the same shift.  The weights are computed before
+//    (v_permlane16/32_swap, no LDS round trip).  The weights are computed before
 //    that (rare) branch, assuming no max moves, so the exponentials overlap the
 //    next tile's score MFMAs; the PV MFMA burst runs at raised wave priority.
 //    Exponentials use the raw v_exp_f32; tiles wholly below the causal
@@ -415,7 +417,14 @@ prefill_kernel(PrefillArgs a) {
     pp = read_pages(3);
 
     // ---- Q^T operands: lane (g,c) of block b holds column col0 + 16b + c ----
-    h8 qh[NB][4];
+    // x = q * (1/sqrt(HD) * log2 e) is split x = hi + lo into two fp16 terms
+    // after scaling the column by a power of two up = 2^k (the column's largest
+    // |x| lands in [2^14, 2^15)), so lo keeps the bits hi drops (~2^-22 of the
+    // column's scale instead of fp16's 2^-11) and stays a normal number; the
+    // score MFMAs run once per term, and the scores come out multiplied by up,
+    // which qf = 1/up undoes per lane.
+    h8 qh[NB][4], ql[NB][4];
+    float qf[NB];
     int qpos[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
@@ -425,23 +434,43 @@ prefill_kernel(PrefillArgs a) {
         const int hh = real ? col - qi * G : 0;
         qpos[b] = real ? n_past + qi : -1;
         const float* qp = qs + ((int64_t)qi * NH + kvh * G + hh) * HD + 8 * g;
+        float xv[4][8];
+        float amax = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const f4 x0 = *reinterpret_cast<const f4*>(qp + 32 * ks);
             const f4 x1 = *reinterpret_cast<const f4*>(qp + 32 * ks + 4);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                qh[b][ks][j] = (_Float16)(real ? x0[j] * (kScale * kLog2e) : 0.f);
-                qh[b][ks][4 + j] = (_Float16)(real ? x1[j] * (kScale * kLog2e) : 0.f);
+                xv[ks][j] = real ? x0[j] * (kScale * kLog2e) : 0.f;
+                xv[ks][4 + j] = real ? x1[j] * (kScale * kLog2e) : 0.f;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(xv[ks][j]));
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));   // the column's 128 dims sit in lanes c, c+16, c+32, c+48
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        int ex = 0;
+        if (amax > 0.f) (void)frexpf(amax, &ex);
+        const int k2 = amax > 0.f ? 15 - ex : 0;
+        const float up = ldexpf(1.f, k2);
+        qf[b] = ldexpf(1.f, -k2);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = xv[ks][j] * up;
+                const _Float16 h = (_Float16)x;
+                qh[b][ks][j] = h;
+                ql[b][ks][j] = (_Float16)(x - (float)h);
             }
         }
     }
 
-    // Running max m of the lane's column (log2 units), kept as -m in the four
-    // lanes' accumulator seeds: the score MFMAs start from -m, so they produce
-    // s - m directly.  m starts at 0; the wave's first tile always rescales.
+    // Running max m of the lane's column (log2 units); x = s - m is formed as
+    // one fma of the raw (scaled) MFMA score with qf and -m.  m starts at 0;
+    // the wave's first tile always rescales.
     float m[NB];
-    f4 negm[NB];
     f4 lsum[NB];          // row sums from the matrix core: every element = l of column c
     f4 acc[NB][8];
     h8 ones;
@@ -450,7 +479,6 @@ prefill_kernel(PrefillArgs a) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         m[b] = 0.f;
-        negm[b] = f4{0.f, 0.f, 0.f, 0.f};
         lsum[b] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) acc[b][cb] = f4{0.f, 0.f, 0.f, 0.f};
@@ -487,8 +515,10 @@ prefill_kernel(PrefillArgs a) {
             const h8 k1 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + koff[ks] + 16 * ROWB));
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
-                s0[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qh[b][ks], ks ? s0[b] : negm[b], 0, 0, 0);
-                s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[b][ks], ks ? s1[b] : negm[b], 0, 0, 0);
+                s0[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qh[b][ks], ks ? s0[b] : f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[b][ks], ks ? s1[b] : f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                s0[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, ql[b][ks], s0[b], 0, 0, 0);
+                s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, ql[b][ks], s1[b], 0, 0, 0);
             }
         }
     };
@@ -521,8 +551,8 @@ prefill_kernel(PrefillArgs a) {
         for (int b = 0; b < NB; ++b) {
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-                x[b][ii] = c0[b][ii];
-                x[b][4 + ii] = c1[b][ii];
+                x[b][ii] = fmaf(c0[b][ii], qf[b], -m[b]);
+                x[b][4 + ii] = fmaf(c1[b][ii], qf[b], -m[b]);
             }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
@@ -567,9 +597,6 @@ prefill_kernel(PrefillArgs a) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
                     ph[b][j] = (_Float16)(ok[b][j] ? __builtin_amdgcn_exp2f(x[b][j] - shift) : 0.f);
-                n0[b] -= shift;                  // the next tile's scores were seeded with the old max
-                n1[b] -= shift;
-                negm[b] = f4{-m[b], -m[b], -m[b], -m[b]};
             }
         }
         __builtin_amdgcn_s_setprio(1);   // the PV MFMAs go first on the SIMD
@@ -678,6 +705,10 @@ int compute_units() {
 #ifndef NOVA_PREFILL_KS_NARROW
 #define NOVA_PREFILL_KS_NARROW 2
 #endif
+#ifndef NOVA_PREFILL_NB_WIDE
+#define NOVA_PREFILL_NB_WIDE 2
+#endif
+constexpr int kNbWide = NOVA_PREFILL_NB_WIDE;      // 16-column blocks per wave in wide launches
 constexpr int kKsWide = NOVA_PREFILL_KS_WIDE;      // key groups with 128-column workgroups
 constexpr int kKsNarrow = NOVA_PREFILL_KS_NARROW;  // and with 64-column workgroups
 
@@ -690,12 +721,12 @@ void launch(const PrefillArgs& a, int n_sess, hipStream_t s) {
     const int64_t slots = (int64_t)compute_units() * (2 / kKsWide);
     const int64_t items128 = (a.n_q * G + 127) / 128 * (int64_t)n_sess * NKV;
     const bool wide = items128 >= slots;
-    const int cols_wg = wide ? 128 : 64;
+    const int cols_wg = wide ? 64 * kNbWide : 64;
     const int64_t n_cg = (a.n_q * G + cols_wg - 1) / cols_wg;
     const int64_t n_wg = (n_cg * n_sess * NKV + kXcd - 1) / kXcd * kXcd;
     NOVA_REQUIRE(n_wg < (int64_t)1 << 31);
     if (wide)
-        hipLaunchKernelGGL((prefill_kernel<2, kKsWide>), dim3((unsigned)n_wg), dim3(THREADS * kKsWide), 0, s, a);
+        hipLaunchKernelGGL((prefill_kernel<kNbWide, kKsWide>), dim3((unsigned)n_wg), dim3(THREADS * kKsWide), 0, s, a);
     else
         hipLaunchKernelGGL((prefill_kernel<1, kKsNarrow>), dim3((unsigned)n_wg), dim3(THREADS * kKsNarrow), 0, s, a);
     NOVA_LAUNCHED();

@@ -73,6 +73,7 @@ _SIGS = {
     "launch_attn_decode_paged_rope_batch": (None, [vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp]),
     "launch_attn_decode_paged_batch": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp, vp, vp]),
     "launch_attn_decode_paged_batch_noalloc": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp, vp]),
+    "testkit_attn_decode_split_only": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp]),
     "launch_attn_decode_plan": (None, [vp, i32, vp, i32, vp, vp]),
     "launch_attn_decode_paged_planned": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]),
     "launch_attn_prefill_paged_batch": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp]),

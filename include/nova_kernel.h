@@ -128,6 +128,13 @@ void launch_attn_decode_paged_rope_batch(const float* q, const float* k_new, con
                                          int n_sess, int layer, int nb, float* o, void* workspace,
                                          nova_stream_t s);
 
+/* Test kit (not a reference surface): only the split kernel of
+ * launch_attn_decode_paged_planned -- partials written, o not -- so that a
+ * benchmark can time the dominant kernel alone on its own stream. */
+void testkit_attn_decode_split_only(const float* q, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
+                                    int table_stride, int n_sess, int layer, int nb, const uint16_t* k_new,
+                                    const uint16_t* v_new, void* workspace, nova_stream_t s);
+
 /* Batched append: session i writes n tokens at positions pos0[i]..pos0[i]+n-1
  * (pos0: device int32[n_sess]) through tables + i*table_stride; k, v:
  * [n_sess][n][NKV][HD] fp16.  One launch for a decode step's appends (or a

@@ -45,9 +45,9 @@
 //    once into hi + lo fp16 terms, each with its own score MFMA, so scores
 //    carry ~2^-22 relative error per operand instead of fp16's 2^-11 (real
 //    post-RoPE queries are far from unit scale); P is fp16; accumulation is
-//    fp32.  The row sums l come from the matrix core too
-//    (one MFMA of an all-ones operand with P^T per block), so they are the
-//    sums of exactly the fp16 weights applied to V, at no VALU cost.
+//    fp32.  The row sums l are sums of exactly the fp16 weights applied to V
+//    (four v_dot2 per lane and block against (1, 1), reduced over the column's
+//    four lanes at the end).
 //  * Lazy rescaling: a column's running max m only moves when a tile's max
 //    exceeds it by more than 8 (log2 units), bounding P by 2^8 in fp16, so the
 //    O rescale (32 multiplies per block) is skipped on most tiles.  Each score
@@ -82,6 +82,7 @@ namespace nova {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
@@ -471,15 +472,12 @@ prefill_kernel(PrefillArgs a) {
     // one fma of the raw (scaled) MFMA score with qf and -m.  m starts at 0;
     // the wave's first tile always rescales.
     float m[NB];
-    f4 lsum[NB];          // row sums from the matrix core: every element = l of column c
+    float lsum[NB];       // this lane's share (its 8 keys of each tile) of column c's row sum
     f4 acc[NB][8];
-    h8 ones;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ones[j] = (_Float16)1.0f;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         m[b] = 0.f;
-        lsum[b] = f4{0.f, 0.f, 0.f, 0.f};
+        lsum[b] = 0.f;
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) acc[b][cb] = f4{0.f, 0.f, 0.f, 0.f};
     }
@@ -572,10 +570,13 @@ prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) ph[b][j] = (_Float16)(ok[b][j] ? __builtin_amdgcn_exp2f(x[b][j]) : 0.f);
         // score MFMAs of the next tile interleaved with the work above
+#ifndef NOVA_PREFILL_SCHED_VALU
+#define NOVA_PREFILL_SCHED_VALU 3
+#endif
 #pragma unroll
-        for (int i = 0; i < 8 * NB; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // three VALU
+        for (int i = 0; i < 16 * NB; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA (hi or lo term)
+            __builtin_amdgcn_sched_group_barrier(0x002, NOVA_PREFILL_SCHED_VALU, 0);
         }
         bool over = false;
 #pragma unroll
@@ -602,8 +603,12 @@ prefill_kernel(PrefillArgs a) {
         __builtin_amdgcn_s_setprio(1);   // the PV MFMAs go first on the SIMD
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            // l += ones . P^T: the sum of exactly the fp16 weights applied below
-            lsum[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, ph[b], lsum[b], 0, 0, 0);
+            // l += the lane's 8 fp16 weights, exactly those applied below,
+            // summed in fp32 by four v_dot2 against (1, 1)
+#pragma unroll
+            for (int j = 0; j < 8; j += 2)
+                lsum[b] = __builtin_amdgcn_fdot2(h2{ph[b][j], ph[b][j + 1]}, h2{(_Float16)1.0f, (_Float16)1.0f},
+                                                 lsum[b], false);
 #pragma unroll
             for (int cb = 0; cb < 8; ++cb)
                 acc[b][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[cb], ph[b], acc[b][cb], 0, 0, 0);
@@ -646,6 +651,13 @@ prefill_kernel(PrefillArgs a) {
         if (i + 3 < n_steps) step(std::integral_constant<int, 3>{}, i + 3, sb0, sb1, sa0, sa1);
     }
 
+    // the column's row sum over its four 16-lane rows
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        lsum[b] += __shfl_xor(lsum[b], 16, 64);
+        lsum[b] += __shfl_xor(lsum[b], 32, 64);
+    }
+
     if constexpr (KS == 2) {
         // merge group 1's (m, l, acc) into group 0's through LDS (the tile
         // buffers are free: the last step ended with a barrier)
@@ -655,7 +667,7 @@ prefill_kernel(PrefillArgs a) {
             for (int b = 0; b < NB; ++b) {
 #pragma unroll
                 for (int cb = 0; cb < 8; ++cb) *reinterpret_cast<f4*>(xs + b * 34 + 4 * cb) = acc[b][cb];
-                xs[b * 34 + 32] = lsum[b][0];
+                xs[b * 34 + 32] = lsum[b];
                 xs[b * 34 + 33] = m[b];
             }
         }
@@ -663,7 +675,7 @@ prefill_kernel(PrefillArgs a) {
         if (kg == 1) return;
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            const float l1 = xs[b * 34 + 32], m1 = xs[b * 34 + 33], l0 = lsum[b][0];
+            const float l1 = xs[b * 34 + 32], m1 = xs[b * 34 + 33], l0 = lsum[b];
             // a group without keys for this column has l = 0 and must not set the max
             const float mm = l1 > 0.f ? (l0 > 0.f ? fmaxf(m[b], m1) : m1) : m[b];
             const float f0 = l0 > 0.f ? __builtin_amdgcn_exp2f(m[b] - mm) : 0.f;
@@ -671,14 +683,14 @@ prefill_kernel(PrefillArgs a) {
 #pragma unroll
             for (int cb = 0; cb < 8; ++cb)
                 acc[b][cb] = acc[b][cb] * f0 + *reinterpret_cast<const f4*>(xs + b * 34 + 4 * cb) * f1;
-            lsum[b] = f4{1.f, 1.f, 1.f, 1.f} * (l0 * f0 + l1 * f1);
+            lsum[b] = l0 * f0 + l1 * f1;
         }
     }
 
     // ---- normalise and store: lane (g,c) of block b holds d = 16cb + 4g + i ----
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-        const float L = lsum[b][0];
+        const float L = lsum[b];
         const int col = col0 + 16 * b + c;
         if (col >= n_cols) continue;
         const int qi = col / G, hh = col - qi * G;

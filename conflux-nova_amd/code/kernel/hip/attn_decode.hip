@@ -1077,8 +1077,12 @@ DecodeArgs batch_args(const int32_t* tables, int table_stride, const int32_t* n_
     a.gw = batch_workgroups();
     a.plan = static_cast<const int32_t*>(workspace);
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan_bytes(n_sess));
+    // Partial slots: with two waves per kv head (7B) they merge through LDS
+    // into one slot per workgroup (half the partial bytes, same step time);
+    // with four (1.5B) the exchange costs more than it saves: one slot per
+    // wave row (measured on config 1: 8.5 vs 6.4 us per split launch).
 #ifndef NOVA_DECODE_PART_MODE
-#define NOVA_DECODE_PART_MODE 2
+#define NOVA_DECODE_PART_MODE (R == 2 ? 2 : 1)
 #endif
     a.wave_parts = R > 1 ? NOVA_DECODE_PART_MODE : 1;
     return a;

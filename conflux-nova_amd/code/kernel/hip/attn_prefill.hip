@@ -511,10 +511,15 @@ prefill_kernel(PrefillArgs a) {
         for (int ks = 0; ks < 4; ++ks) {
             const h8 k0 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + koff[ks]));
             const h8 k1 = __builtin_bit_cast(h8, *reinterpret_cast<const u4*>(sk + koff[ks] + 16 * ROWB));
+            // the hi terms of every accumulator, then the lo terms: 2*NB
+            // independent MFMAs between two that share an accumulator
 #pragma unroll
             for (int b = 0; b < NB; ++b) {
                 s0[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, qh[b][ks], ks ? s0[b] : f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, qh[b][ks], ks ? s1[b] : f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            }
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
                 s0[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k0, ql[b][ks], s0[b], 0, 0, 0);
                 s1[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(k1, ql[b][ks], s1[b], 0, 0, 0);
             }

@@ -329,6 +329,7 @@ decode_split_kernel(DecodeArgs a) {
     __shared__ float s_acc[(R > 1 || kKvSplit) ? WAVES : 1][G][HD];
     __shared__ u4 s_q[NKV][4][2][64];            // Q^T hi/lo operands per kv head
     __shared__ float s_qf[NKV][16];              // per-head score factor
+    __shared__ int s_ready[WAVES];               // a wave's exchange rows are in LDS (one-slot partials)
 
     const int tid = threadIdx.x;
     const int wave = tid >> 6;
@@ -555,6 +556,7 @@ decode_split_kernel(DecodeArgs a) {
                 s_q[kvh][ks][1][lane] = __builtin_bit_cast(u4, lo);
             }
         }
+        if (lane == 0) s_ready[wave] = 0;
         __syncthreads();
         if (wave == 0) TRACE(1);
         const float qf = s_qf[kvh][c];
@@ -703,7 +705,21 @@ decode_split_kernel(DecodeArgs a) {
                     *reinterpret_cast<f4*>(&s_acc[wave][c][8 * (4 * g + ii) + 4]) = hi4;
                 }
             }
-            __syncthreads();
+            // publish to the other waves of this kv head only (no workgroup
+            // barrier: a wave waits for its R - 1 partners, not for the
+            // slowest wave of the workgroup); bounded wait, every wave of the
+            // workgroup reaches this point
+            if (lane == 0) __hip_atomic_store(&s_ready[wave], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+#pragma unroll
+            for (int rr = 0; rr < R; ++rr) {
+                const int ww = kvh + NKV * rr;
+                if (ww == wave) continue;
+                for (int it = 0; it < (1 << 22); ++it) {
+                    const int f = __hip_atomic_load(&s_ready[ww], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    if (__builtin_amdgcn_readfirstlane(f)) break;
+                    __builtin_amdgcn_s_sleep(1);
+                }
+            }
             if (keeper == r && c < G) {
                 float M = -INFINITY;
 #pragma unroll

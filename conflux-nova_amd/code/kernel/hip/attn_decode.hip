@@ -162,9 +162,9 @@ __device__ __forceinline__ u4 ld16_nt(const char* base, uint32_t off) {
 }
 
 #ifdef NOVA_DECODE_TRACE
-// per-workgroup timeline (development builds only): 8 x 64-bit per workgroup slot
-__device__ uint64_t g_trace[2048 * 8];
-#define TRACE(k) do { if ((threadIdx.x & 63) == 0) g_trace[(int64_t)blockIdx.x * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+// per-workgroup timeline (development builds only): 8 x 64-bit per (layer, workgroup slot)
+__device__ uint64_t g_trace[64 * 512 * 8];
+#define TRACE(k) do { if ((threadIdx.x & 63) == 0 && blockIdx.x < 512) g_trace[((int64_t)(a.layer & 63) * 512 + blockIdx.x) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
 #else
 #define TRACE(k) do {} while (0)
 #endif
@@ -1064,8 +1064,12 @@ int batch_workgroups() {
 }
 
 void launch_split(const DecodeArgs& a, int n_sess, hipStream_t st) {
+#ifdef NOVA_DECODE_GRID_OVERRIDE
+    const dim3 grid = a.kv_split ? dim3(NKV, a.gw + n_sess) : dim3(NOVA_DECODE_GRID_OVERRIDE);
+#else
     const dim3 grid = a.kv_split ? dim3(NKV, a.gw + n_sess)
                                  : dim3(a.plan ? split_slots(n_sess, a.gw) : a.gw + n_sess);
+#endif
     if (a.kv_split) hipLaunchKernelGGL((decode_split_kernel<false, true>), grid, dim3(THREADS), 0, st, a);
     else if (a.cs) hipLaunchKernelGGL((decode_split_kernel<true, false>), grid, dim3(THREADS), 0, st, a);
     else hipLaunchKernelGGL((decode_split_kernel<false, false>), grid, dim3(THREADS), 0, st, a);

@@ -463,6 +463,32 @@ decode_split_kernel(DecodeArgs a) {
                 qraw[2 * ks + 1] = *reinterpret_cast<const f4*>(qp + step * (32 * ks + 4));
             }
         }
+        // fused RoPE: the cos/sin row of position n_keys - 1 for this lane's q
+        // dims, and this thread's piece of the new k (one NeoX pair) and v
+        f4 rcs[4], rsn[4];
+        float rk0 = 0.f, rk1 = 0.f, rc = 0.f, rs = 0.f;
+        float2 rv = {0.f, 0.f};
+        static_assert(!kRope || (NKV * (HD / 2) <= THREADS && KVW <= 2 * THREADS), "one k pair and two v values per thread");
+        const bool rope_k = kRope && appends && tid < NKV * (HD / 2);
+        const bool rope_v = kRope && appends && 2 * tid < KVW;
+        if constexpr (kRope) {
+            const int64_t row = (int64_t)(n_keys - 1) * (HD / 2);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                rcs[2 * ks] = *reinterpret_cast<const f4*>(a.cs + row + 32 * ks + 8 * g);
+                rcs[2 * ks + 1] = *reinterpret_cast<const f4*>(a.cs + row + 32 * ks + 8 * g + 4);
+                rsn[2 * ks] = *reinterpret_cast<const f4*>(a.sn + row + 32 * ks + 8 * g);
+                rsn[2 * ks + 1] = *reinterpret_cast<const f4*>(a.sn + row + 32 * ks + 8 * g + 4);
+            }
+            const int h = tid / (HD / 2), d = tid - h * (HD / 2);
+            const int64_t kr = rope_k ? (int64_t)i * KVW + h * HD + d : 0;
+            rk0 = a.k_new32[kr];
+            rk1 = a.k_new32[kr + HD / 2];
+            rc = a.cs[row + (rope_k ? d : 0)];
+            rs = a.sn[row + (rope_k ? d : 0)];
+            rv = *reinterpret_cast<const float2*>(a.v_new32 + (rope_v ? (int64_t)i * KVW + 2 * tid : 0));
+        }
+        asm volatile("" ::: "memory");   // keep the loads above ahead of the pair's in issue order
         PairRegs cur;
         static_assert(2 * (8 - 1) + 1 < 64, "a first pair lies in the slice register");
         // the first pair (a wave without one, or whose pair the append is about
@@ -480,18 +506,18 @@ decode_split_kernel(DecodeArgs a) {
                 // n_keys - 1, k and v rounded to fp16 (nearest even)
                 uint16_t* pk16 = const_cast<uint16_t*>(a.pool_k) + dst;
                 uint16_t* pv16 = const_cast<uint16_t*>(a.pool_v) + dst;
-                const float* crow = a.cs + (int64_t)(n_keys - 1) * (HD / 2);
-                const float* srow = a.sn + (int64_t)(n_keys - 1) * (HD / 2);
-                for (int e = tid; e < NKV * (HD / 2); e += THREADS) {
-                    const int h = e / (HD / 2), d = e - h * (HD / 2);
-                    const float* kr = a.k_new32 + src + h * HD;
+                (void)src;
+                if (rope_k) {
+                    const int h = tid / (HD / 2), d = tid - h * (HD / 2);
                     float y0, y1;
-                    rope_rotate(kr[d], kr[d + HD / 2], crow[d], srow[d], y0, y1);
+                    rope_rotate(rk0, rk1, rc, rs, y0, y1);
                     pk16[h * HD + d] = __builtin_bit_cast(uint16_t, (_Float16)y0);
                     pk16[h * HD + d + HD / 2] = __builtin_bit_cast(uint16_t, (_Float16)y1);
                 }
-                for (int e = tid; e < KVW; e += THREADS)
-                    pv16[e] = __builtin_bit_cast(uint16_t, (_Float16)a.v_new32[src + e]);
+                if (rope_v) {
+                    pv16[2 * tid] = __builtin_bit_cast(uint16_t, (_Float16)rv.x);
+                    pv16[2 * tid + 1] = __builtin_bit_cast(uint16_t, (_Float16)rv.y);
+                }
             } else if (app_thread) {
                 (void)src;
                 *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_k) + dst + 8 * tid) = knew;
@@ -517,14 +543,13 @@ decode_split_kernel(DecodeArgs a) {
                 // RoPE of q at position n_keys - 1: lane (g,c) holds dims
                 // 32ks + 8g + jj, so the pair (d, d + 64) is (ks, ks + 2) in
                 // the same lane; the caller's q is left as it is
-                const float* crow = a.cs + (int64_t)(n_keys - 1) * (HD / 2) + 8 * g;
-                const float* srow = a.sn + (int64_t)(n_keys - 1) * (HD / 2) + 8 * g;
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
                     for (int jj = 0; jj < 8; ++jj) {
                         float y0, y1;
-                        rope_rotate(qv[ks][jj], qv[ks + 2][jj], crow[32 * ks + jj], srow[32 * ks + jj], y0, y1);
+                        rope_rotate(qv[ks][jj], qv[ks + 2][jj], rcs[2 * ks + (jj >> 2)][jj & 3],
+                                    rsn[2 * ks + (jj >> 2)][jj & 3], y0, y1);
                         qv[ks][jj] = y0;
                         qv[ks + 2][jj] = y1;
                     }

@@ -649,6 +649,10 @@ prefill_kernel(PrefillArgs a) {
         if (ahead) tile_barrier<LOADS>();
         else tile_barrier<0>();
     };
+#ifdef NOVA_PREFILL_PHASE
+    // development: offset the phase of alternate workgroups by about half a tile
+    if (blockIdx.x & NOVA_PREFILL_PHASE) __builtin_amdgcn_s_sleep(12);
+#endif
     for (int i = 0; i < n_steps; i += NBUF) {               // unrolled: buffers and score registers rotate
         step(std::integral_constant<int, 0>{}, i, sa0, sa1, sb0, sb1);
         if (i + 1 < n_steps) step(std::integral_constant<int, 1>{}, i + 1, sb0, sb1, sa0, sa1);

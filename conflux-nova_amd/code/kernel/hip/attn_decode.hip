@@ -13,13 +13,15 @@
 //    session.  Every workgroup does at most that share whatever
 //    the context lengths, so
 //    a ragged batch fills all CUs evenly, and a workgroup never straddles two
-//    sessions.  Each workgroup writes one partial (m, l, acc[HD]) per head
-//    and wave row in the batched path (the combine merges the wave rows with
-//    the workgroups: measured 0.8465 -> 0.8345 ms per config-2 step against
-//    merging them in LDS behind a barrier first, although the partial bytes
-//    double), one per head in the reference-signature path (its scratch holds
-//    32 rows per head; there each page range runs as NKV workgroups, one per
-//    kv head, so one single-session call spreads over 31 * NKV CUs).
+//    sessions.  In the batched path a workgroup writes one partial
+//    (m, l, acc[HD]) per head: with two waves per kv head (7B) the two merge
+//    through LDS first, each keeping half of the head dims and signalling the
+//    other with an LDS flag rather than a workgroup barrier; with four (1.5B)
+//    each wave row writes its own slot (the four-way exchange costs more than
+//    the bytes it saves).  The reference-signature path writes one partial per
+//    head and page range (its scratch holds 32 rows per head; there each page
+//    range runs as NKV workgroups, one per kv head, so one single-session call
+//    spreads over 31 * NKV CUs).
 //    Every wave derives the partition itself from one load of n_keys.
 //  * One workgroup = 8 wave64s, one workgroup per CU.  Wave w serves kv head
 //    w % NKV and takes every R-th pair of pages (R = 8/NKV), so the workgroup
@@ -28,7 +30,11 @@
 //    query operands live once per kv head in LDS.
 //  * Latency hiding inside a wave: the segment's block-table slice is fetched
 //    once (one coalesced load, then v_readlane per page), so no pair waits on
-//    a table lookup.
+//    a table lookup.  Every wave issues its loads in one fixed order -- the
+//    appended token's page and row, the query rows (and the RoPE rows), then
+//    its first pair -- so that the vector-memory counter, which drains in
+//    issue order, lets the query conversion and the append wait only for what
+//    they use, not for the pair.
 //    Page bases are wave-uniform (SGPR) and lane
 //    offsets are fixed 32-bit values, so the loop does no per-lane 64-bit
 //    address arithmetic.

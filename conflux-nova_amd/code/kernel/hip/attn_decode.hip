@@ -1095,12 +1095,8 @@ int batch_workgroups() {
 }
 
 void launch_split(const DecodeArgs& a, int n_sess, hipStream_t st) {
-#ifdef NOVA_DECODE_GRID_OVERRIDE
-    const dim3 grid = a.kv_split ? dim3(NKV, a.gw + n_sess) : dim3(NOVA_DECODE_GRID_OVERRIDE);
-#else
     const dim3 grid = a.kv_split ? dim3(NKV, a.gw + n_sess)
                                  : dim3(a.plan ? split_slots(n_sess, a.gw) : a.gw + n_sess);
-#endif
     if (a.kv_split) hipLaunchKernelGGL((decode_split_kernel<false, true>), grid, dim3(THREADS), 0, st, a);
     else if (a.cs) hipLaunchKernelGGL((decode_split_kernel<true, false>), grid, dim3(THREADS), 0, st, a);
     else hipLaunchKernelGGL((decode_split_kernel<false, false>), grid, dim3(THREADS), 0, st, a);

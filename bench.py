@@ -183,8 +183,10 @@ class DecodeWorkload:
 
     def kernel_times(self, reps=20):
         """Average duration (ms) of one layer's decode launch pair (split +
-        combine: one launch_attn_decode_paged_planned call) and of the split
-        kernel alone (testkit_attn_decode_split_only), each from a HIP graph of
+        combine: one launch_attn_decode_paged_planned call), of the split
+        kernel alone (testkit_attn_decode_split_only) and of the stream floor
+        (testkit_decode_stream_floor: the same grid reading the same pages
+        with no arithmetic), each from a HIP graph of
         the 28 layers' launches replayed `reps` times and timed with events on
         the stream the kernels run on -- the same replay as the timed step,
         minus the once-per-step plan kernel."""
@@ -196,8 +198,12 @@ class DecodeWorkload:
                 self.q.ptr + l * qs * 4, self.k.ptr, self.v.ptr, self.tables.ptr, self.max_pages, self.n, l, self.nb,
                 self.knew.ptr + l * kvs * 2, self.vnew.ptr + l * kvs * 2, self.ws.ptr, s)
 
+        def floor(l):
+            nv.testkit_decode_stream_floor(self.k.ptr, self.v.ptr, self.tables.ptr, self.max_pages, self.n, l,
+                                           self.nb, self.ws.ptr, s)
+
         out = {}
-        for name, fn in (("pair", self.launch_layer), ("split", split_only)):
+        for name, fn in (("pair", self.launch_layer), ("split", split_only), ("floor", floor)):
             nv.dev_graph_begin(s)
             for l in range(L):
                 fn(l)
@@ -210,7 +216,7 @@ class DecodeWorkload:
                 nv.dev_graph_launch(g, s)
             out[name] = t.stop() / (reps * L)
             nv.dev_graph_destroy(g)
-        return out["pair"], out["split"]
+        return out["pair"], out["split"], out["floor"]
 
     def per_session_ms(self, steps, warmup):
         """The reference's call pattern for the same step (Engine::decode_batch,
@@ -353,7 +359,7 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
     nova.dev_sync()
     bytes_step = wl.bytes_per_step()
     gbs = bytes_step / (ms * 1e-3) / 1e9
-    pair_ms, split_ms = wl.kernel_times()
+    pair_ms, split_ms, floor_ms = wl.kernel_times()
     bytes_launch = bytes_step / wl.layers
     split_gbs = bytes_launch / (split_ms * 1e-3) / 1e9
     pair_gbs = bytes_launch / (pair_ms * 1e-3) / 1e9
@@ -365,9 +371,13 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
             "launch_pair_us": round(pair_ms * 1e3, 2),
             "launch_pair_frac": round(pair_gbs / HBM_PEAK_GBS, 4),
             "step_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "stream_floor_us": round(floor_ms * 1e3, 2),
+            "stream_floor_frac": round(bytes_launch / (floor_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "timing": "HIP events around graph replays of the 28 layers' launches: split kernel alone "
-                      "(testkit_attn_decode_split_only) and the split + combine pair "
-                      "(launch_attn_decode_paged_planned); step_frac = the timed step incl. the plan kernel"}
+                      "(testkit_attn_decode_split_only), the split + combine pair "
+                      "(launch_attn_decode_paged_planned) and the stream floor (testkit_decode_stream_floor: "
+                      "the split grid reading the same pages with the same loads, no arithmetic); "
+                      "step_frac = the timed step incl. the plan kernel"}
     cpu = None
     parity = None
     if not args.no_cpu:

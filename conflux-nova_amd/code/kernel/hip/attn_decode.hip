@@ -859,6 +859,68 @@ decode_split_kernel(DecodeArgs a) {
 #endif
 }
 
+// Stream floor (test kit): the planned split grid reading exactly the split
+// kernel's bytes -- the same plan records, page pairs per wave row, lane
+// offsets and non-temporal 16-byte loads -- with no arithmetic but a running
+// sum, one 4-byte word per thread stored into the partial area.  Its time is
+// the HBM floor of this partition on the part, to set the split kernel's
+// time against.
+__global__ void __launch_bounds__(THREADS)
+decode_stream_floor_kernel(DecodeArgs a) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4, c = lane & 15;
+    const int kvh = wave % NKV, r = wave / NKV;
+    const int w = (int)blockIdx.x;
+    const int32_t* rec = a.plan + plan_rec_off(a.n_sess) + (int64_t)w * kRec;
+    int tv = rec[lane];
+    const int hv = rec[kRecPages + (lane & 7)];
+    const int i = __builtin_amdgcn_readlane(hv, 0);
+    if (i < 0) return;
+    const int pa = __builtin_amdgcn_readlane(hv, 1);
+    const int pb = __builtin_amdgcn_readlane(hv, 2);
+    const int32_t* table = a.tables + (int64_t)i * a.table_stride;
+    const uint32_t koff = (uint32_t)((c & 7) * kRowBytes + kvh * HD * 2 + 16 * (g + 4 * (c >> 3)));
+    uint32_t voff[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) voff[jj] = (uint32_t)((4 * g + jj) * kRowBytes + kvh * HD * 2 + 16 * c);
+    const char* pk = reinterpret_cast<const char*>(a.pool_k);
+    const char* pv = reinterpret_cast<const char*>(a.pool_v);
+    const int64_t layer_page0 = (int64_t)a.layer * a.nb;
+    int tchunk = 0;
+    auto phys_of = [&](int pg) -> int {
+        const int rel = pg - pa;
+        if ((rel >> 6) != tchunk) {
+            tchunk = rel >> 6;
+            const int e = pa + 64 * tchunk + lane;
+            tv = e < pb ? table[e] : 0;
+        }
+        return __builtin_amdgcn_readlane(tv, rel & 63);
+    };
+    u4 sum = {0u, 0u, 0u, 0u};
+    const int npairs = (pb - pa + 1) >> 1;
+    for (int qp = r; qp < npairs; qp += R) {
+        const int pg0 = pa + 2 * qp;
+        const int pg1 = pg0 + 1 < pb ? pg0 + 1 : pg0;
+        const int64_t b0 = (layer_page0 + phys_of(pg0)) * kPageBytes;
+        const int64_t b1 = (layer_page0 + phys_of(pg1)) * kPageBytes;
+        u4 x[16];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const uint32_t o = koff + (ks & 1) * 8 * kRowBytes + (ks >> 1) * 128;
+            x[ks] = ld16_nt(pk + b0, o);
+            x[4 + ks] = ld16_nt(pk + b1, o);
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            x[8 + jj] = ld16_nt(pv + b0, voff[jj]);
+            x[12 + jj] = ld16_nt(pv + b1, voff[jj]);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sum += x[e];
+    }
+    reinterpret_cast<uint32_t*>(a.part)[(int64_t)w * THREADS + tid] = sum[0] + sum[1] + sum[2] + sum[3];
+}
+
 // Combine: one workgroup per (session, head) merges the session's k_i
 // partials (slots kc_i .. kc_i+k_i-1) with the rule of fa_combine_kernel
 // (attn.cu:163-191): M = max m_s, L = sum over l_s > 0 of l_s*2^(m_s-M),
@@ -1227,6 +1289,21 @@ void testkit_attn_decode_split_only(const float* q, uint16_t* pool_k, uint16_t* 
     a.k_new = k_new;
     a.v_new = v_new;
     launch_split(a, n_sess, reinterpret_cast<hipStream_t>(s));
+}
+
+void testkit_decode_stream_floor(const uint16_t* pool_k, const uint16_t* pool_v, const int32_t* tables,
+                                 int table_stride, int n_sess, int layer, int nb, void* workspace, nova_stream_t s) {
+    NOVA_REQUIRE(pool_k && pool_v);
+    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0);
+    DecodeArgs a = batch_args(tables, table_stride, nullptr, n_sess, workspace);
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.layer = layer;
+    a.nb = nb;
+    static_assert(THREADS <= R * NH * PW, "one sink word per thread fits in a workgroup's partial slots");
+    hipLaunchKernelGGL(decode_stream_floor_kernel, dim3(split_slots(n_sess, a.gw)), dim3(THREADS), 0,
+                       reinterpret_cast<hipStream_t>(s), a);
+    NOVA_LAUNCHED();
 }
 
 void launch_attn_decode_paged_rope_planned(const float* q, const float* k_new, const float* v_new, const float* cs,

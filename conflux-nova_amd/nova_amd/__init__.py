@@ -74,6 +74,7 @@ _SIGS = {
     "launch_attn_decode_paged_batch": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp, vp, vp]),
     "launch_attn_decode_paged_batch_noalloc": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp, vp]),
     "testkit_attn_decode_split_only": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp]),
+    "testkit_decode_stream_floor": (None, [vp, vp, vp, i32, i32, i32, i32, vp, vp]),
     "launch_attn_decode_plan": (None, [vp, i32, vp, i32, vp, vp]),
     "launch_attn_decode_paged_planned": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]),
     "launch_attn_prefill_paged_batch": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp]),

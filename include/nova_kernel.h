@@ -135,6 +135,13 @@ void testkit_attn_decode_split_only(const float* q, uint16_t* pool_k, uint16_t* 
                                     int table_stride, int n_sess, int layer, int nb, const uint16_t* k_new,
                                     const uint16_t* v_new, void* workspace, nova_stream_t s);
 
+/* Test kit (not a reference surface): the HBM floor of the planned split --
+ * the split grid of launch_attn_decode_paged_planned reading the same pages
+ * with the same loads and no arithmetic (one sink word per thread into the
+ * workspace's partial area).  Needs the step's launch_attn_decode_plan. */
+void testkit_decode_stream_floor(const uint16_t* pool_k, const uint16_t* pool_v, const int32_t* tables,
+                                 int table_stride, int n_sess, int layer, int nb, void* workspace, nova_stream_t s);
+
 /* Batched append: session i writes n tokens at positions pos0[i]..pos0[i]+n-1
  * (pos0: device int32[n_sess]) through tables + i*table_stride; k, v:
  * [n_sess][n][NKV][HD] fp16.  One launch for a decode step's appends (or a

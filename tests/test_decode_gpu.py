@@ -292,3 +292,53 @@ def test_decode_long_ranges():
         assert_close(got[i], ref[i], what=f"batched session {i}")
     one = _decode_single(nova, fx, np.ascontiguousarray(q[1]), np.ascontiguousarray(tables[1]), 40000)
     assert_close(one, _decode_f64(q[1], fx.hk, fx.hv, tables[1], 40000, nova.group), what="single 40000 keys")
+
+
+def test_stream_floor_reads_the_planned_pairs(nova7):
+    """testkit_decode_stream_floor (the bench's HBM floor of the planned split)
+    reads, in every workgroup slot of the plan and every wave, exactly the page
+    pairs that wave of the split kernel reads: with pools of fp16 words 0x0001
+    each thread's sink word is 64 * 0x00010001 per pair it loaded."""
+    nova = nova7
+    n_keys = np.array([700, 33, 1, 2048, 15, 300, 4100, 0, 129], np.int32)
+    n = len(n_keys)
+    max_pages = int((n_keys.max() + 15) // 16)
+    nb = n * max_pages + 4
+    rng = np.random.default_rng(31)
+    page = nova.kb * nova.kvw
+    ones = np.ones(nb * page, np.uint16)
+    k, v = nova.upload(ones), nova.upload(ones)       # layer 0 only
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.ascontiguousarray(perm[: n * max_pages].reshape(n, max_pages))
+    ws_bytes = nova.attn_decode_batch_workspace_bytes(n)
+    ws = nova.alloc(ws_bytes)
+    dt, dn = nova.upload(tables), nova.upload(n_keys)
+    nova.launch_attn_decode_plan(dt.ptr, max_pages, dn.ptr, n, ws.ptr, None)
+    nova.testkit_decode_stream_floor(k.ptr, v.ptr, dt.ptr, max_pages, n, 0, nb, ws.ptr, None)
+    nova.dev_sync()
+    # workspace = plan (rounded to 256 B) + slots * R * NH * PW floats
+    R, PW, rec = 8 // nova.nkv, nova.hd + 2, 72
+    rec_off = n * 4 + n * nova.nh * 4
+    slots = [s for s in range(1, 4096)
+             if -(-(rec_off + s * rec) * 4 // 256) * 256 + s * R * nova.nh * PW * 4 == ws_bytes]
+    assert len(slots) == 1, slots
+    slots = slots[0]
+    plan_b = ws_bytes - slots * R * nova.nh * PW * 4
+    plan = nova.download(ws, (plan_b // 4,), np.int32)
+    sink = nova.download(ws, (slots, 512), np.uint32, plan_b)
+    per_pair = 64 * 0x00010001
+    covered = [np.zeros(int((nk + 15) // 16), np.int32) for nk in n_keys]
+    for w in range(slots):
+        r0 = rec_off + w * rec
+        sess, pa, pb = plan[r0 + 64], plan[r0 + 65], plan[r0 + 66]
+        if sess < 0:          # idle slot
+            continue
+        assert (plan[r0:r0 + min(64, pb - pa)] == tables[sess, pa:pb][:64]).all()
+        covered[sess][pa:pb] += 1
+        npairs = (pb - pa + 1) // 2
+        for wave in range(8):
+            r = wave // nova.nkv
+            want = len(range(r, npairs, R)) * per_pair
+            assert (sink[w, 64 * wave:64 * wave + 64] == want).all(), (w, wave)
+    for i in range(n):
+        assert (covered[i] == 1).all(), i

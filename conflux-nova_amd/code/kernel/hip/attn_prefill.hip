@@ -243,6 +243,26 @@ __device__ __forceinline__ void dma16x4(const void* s0, const void* s1, const vo
         : "memory");
 }
 
+// The same four loads for a tile with no row past the last key: wave-uniform
+// page bases in SGPR pairs (K page 0, K page 1, V page 0, V page 1) and the
+// lane's 32-bit offsets inside a page (one for K, one for V), so the loop
+// keeps two offset registers instead of four 64-bit addresses per tile.
+__device__ __forceinline__ void dma16x4_s(const void* k0, const void* k1, const void* v0, const void* v1,
+                                          uint32_t off_k, uint32_t off_v, uint32_t lds) {
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %7\n\tglobal_load_lds_dwordx4 %5, %1\n\t"
+        "s_mov_b32 m0, %8\n\tglobal_load_lds_dwordx4 %5, %2\n\t"
+        "s_mov_b32 m0, %9\n\tglobal_load_lds_dwordx4 %6, %3\n\t"
+        "s_mov_b32 m0, %10\n\tglobal_load_lds_dwordx4 %6, %4\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(k0), "s"(k1), "s"(v0), "s"(v1), "v"(off_k), "v"(off_v), "s"(lds), "s"(lds + 16u * THREADS),
+          "s"(lds + 32u * THREADS), "s"(lds + 48u * THREADS)
+        : "memory");
+}
+
 // LDS byte address of a __shared__ location
 __device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const unsigned char*)p;
@@ -389,7 +409,7 @@ prefill_kernel(PrefillArgs a) {
         const int64_t b1 = (layer_page0 + __builtin_amdgcn_readfirstlane(pp.p1)) * kPageBytes + kvh * ROWB;
         const uint32_t m0base = __builtin_amdgcn_readfirstlane(lds_addr(&s_kv[kg][BI][0])) + 1024u * wave_s;
         if (TILE * (T + 1) <= key_end) {
-            dma16x4(pk + loff_k + b0, pk + loff_k + b1, pv + loff_v + b0, pv + loff_v + b1, m0base);
+            dma16x4_s(pk + b0, pk + b1, pv + b0, pv + b1, loff_k, loff_v, m0base);
         } else {
             // the tile holding the last key: rows past it (never written, may
             // hold NaN bits) load the last key's row instead; their weights are

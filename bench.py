@@ -13,8 +13,9 @@ resident in HBM before timing starts.  The appended position is the same each
 step (slot ctx_i of session i is rewritten), so every step does identical work.
 
 Output: one JSON line (metric = KV GB/s; ms_per_step; roofline of the decode
-kernel measured with HIP events; cpu_baseline = the C oracle on the host cores
-over one layer of the same workload).
+kernel measured with HIP events; cpu_baseline = oracle/cpu_baseline.c, a
+vectorised, threaded host restatement, on the host cores over one layer of the
+same workload).
 
 Other workloads (--workload): single1p5b (config 1), cow (config 3),
 longctx14b (config 4), prefill (config 5), rope (RoPE fused with the append,
@@ -304,10 +305,14 @@ class DecodeWorkload:
         return out
 
     def cpu_sample(self, layer, threads):
-        """Run the C oracle on the host over one layer; returns (seconds, outputs)."""
-        from oracle_py import Oracle
+        """Run the CPU baseline (oracle/cpu_baseline.c: AVX2/F16C, a thread
+        pool over (session, kv head, 64-page split) units) on the host over
+        one layer; returns (seconds, outputs).  The appended token goes in
+        with the C oracle's append first (untimed)."""
+        from oracle_py import CpuBaseline, Oracle
         nv = self.nova
         orc = Oracle()
+        cpub = CpuBaseline()
         shape = (self.nb, nv.kb, nv.nkv, nv.hd)
         off = layer * self.layer_halves * 2
         pk = nv.download(self.k.ptr + off, shape, np.uint16)
@@ -319,7 +324,7 @@ class DecodeWorkload:
                                np.ascontiguousarray(self.vnew_h[layer, i]))
         q = np.ascontiguousarray(self.q_h[layer])
         secs, out, reps = timed_repeat(
-            lambda: orc.attn_decode_batch(nv.model, q, pk, pv, self.tables_h, self.n_keys, 0, self.nb, threads))
+            lambda: cpub.attn_decode_batch(nv.model, q, pk, pv, self.tables_h, self.n_keys, 0, self.nb, threads))
         self.cpu_reps = reps
         return secs, out
 
@@ -391,8 +396,9 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
             print(f"bench: PARITY FAILURE on layer 0: max|gpu-cpu| = {err:.3e}", file=sys.stderr, flush=True)
         cpu_gbs = (bytes_step / wl.layers) / secs / 1e9
         cpu = {"value": round(cpu_gbs, 3), "unit": "GB/s", "cores": th, "kind": "port",
-               "sample": f"1 of {wl.layers} layers ({cpu_scale_note}); C oracle or_attn_decode_batch, "
-                         f"{secs:.3f} s per call (mean of {wl.cpu_reps}); max|gpu-cpu| on that layer {err:.2e}",
+               "sample": f"1 of {wl.layers} layers ({cpu_scale_note}); cb_attn_decode_batch "
+                         f"(oracle/cpu_baseline.c: AVX2/F16C, {th} threads), "
+                         f"{secs * 1e3:.3f} ms per call (mean of {wl.cpu_reps}, warm host caches); max|gpu-cpu| on that layer {err:.2e}",
                "us_per_step_equiv": round(secs * wl.layers * 1e6, 1)}
     # after the parity leg above: they rewrite the outputs and the appended slots
     per_session = rope = None
@@ -722,23 +728,22 @@ def run_prefill(args):
     tflops = flops / (k_ms * 1e-3) / 1e12
     cpu = parity = None
     if not args.no_cpu:
-        from oracle_py import Oracle
-        orc = Oracle()
+        from oracle_py import CpuBaseline
+        cpub = CpuBaseline()
+        th = cpu_threads(args)
         shape = (nb, nova.kb, nova.nkv, nova.hd)
         pk = nova.download(k, shape, np.uint16)          # layer 0 (chunk already appended)
         pv = nova.download(v, shape, np.uint16)
-        nq_s = 64                                         # bounded sample: first 64 queries of session 0
-        qs = np.ascontiguousarray(q_h[0, :nq_s])
-        secs, ref, reps = timed_repeat(lambda: orc.attn_prefill_paged(
-            "qwen25_7b", qs, pk, pv, np.ascontiguousarray(tables[0]), 0, nb, nq_s, int(n_past[0])))
-        got = nova.download(o, (n_sess, n_q, nova.nh, nova.hd), np.float32)[0, :nq_s]
-        sample_flops = prefill_flops([n_past[0]], nq_s, nova.nh, nova.hd)
-        cpu = {"value": round(sample_flops / secs / 1e12, 6), "unit": "TFLOP/s", "cores": 1, "kind": "port",
-               "sample": f"session 0, first {nq_s} queries, layer 0 (n_past={int(n_past[0])}); C oracle "
-                         f"or_attn_prefill_paged single-threaded, {secs:.2f} s per call (mean of {reps}); "
-                         f"max|gpu-cpu| {float(np.abs(got - ref).max()):.2e}"}
+        q4 = np.ascontiguousarray(q_h.reshape(n_sess, n_q, nova.nh, nova.hd))
+        secs, ref, reps = timed_repeat(lambda: cpub.attn_prefill_batch(
+            "qwen25_7b", q4, pk, pv, tables, n_past, n_q, 0, nb, th))
+        got = nova.download(o, (n_sess, n_q, nova.nh, nova.hd), np.float32)
         perr = float(np.abs(got - ref).max())
-        parity = {"session0_first64_max_abs_err": perr, "ok": perr <= 2e-3}
+        cpu = {"value": round(flops / secs / 1e12, 6), "unit": "TFLOP/s", "cores": th, "kind": "port",
+               "sample": f"layer 0 of 28, all 8 sessions; cb_attn_prefill_batch (oracle/cpu_baseline.c: "
+                         f"AVX2/F16C, {th} threads), {secs * 1e3:.1f} ms per call (mean of {reps}); "
+                         f"max|gpu-cpu| {perr:.2e}"}
+        parity = {"layer0_max_abs_err": perr, "ok": perr <= 2e-3}
         if not parity["ok"]:
             print(f"bench: PARITY FAILURE on prefill: max|gpu-cpu| = {perr:.3e}", file=sys.stderr, flush=True)
     return {

@@ -235,6 +235,38 @@ class Oracle:
         return out
 
 
+class CpuBaseline:
+    """oracle/libcpubase.so: the throughput CPU restatement bench.py times as
+    its cpu_baseline (AVX2/F16C, a thread pool over work units).  Agrees with
+    the oracle to the attention tolerance, not bit for bit."""
+
+    def __init__(self):
+        self.lib = C.CDLL(str(HERE / "libcpubase.so"))
+        self.lib.cb_attn_decode_batch.restype = None
+        self.lib.cb_attn_prefill_batch.restype = None
+
+    def attn_decode_batch(self, model, q, pool_k, pool_v, tables, n_keys, layer, nb, n_threads):
+        g = geom(model)
+        n = len(n_keys)
+        out = np.empty((n, g.nh, g.hd), np.float32)
+        nk = np.ascontiguousarray(n_keys, dtype=np.int32)
+        p = lambda a: a.ctypes.data_as(vp)
+        self.lib.cb_attn_decode_batch(g, p(q), p(pool_k), p(pool_v), p(tables), i32(tables.shape[1]), p(nk),
+                                      i32(n), i32(layer), i32(nb), p(out), i32(n_threads))
+        return out
+
+    def attn_prefill_batch(self, model, q, pool_k, pool_v, tables, n_past, n_q, layer, nb, n_threads):
+        """q [n_sess][n_q][nh][hd] f32; returns o of the same shape."""
+        g = geom(model)
+        n = len(n_past)
+        out = np.empty((n, n_q, g.nh, g.hd), np.float32)
+        npst = np.ascontiguousarray(n_past, dtype=np.int32)
+        p = lambda a: a.ctypes.data_as(vp)
+        self.lib.cb_attn_prefill_batch(g, p(q), p(pool_k), p(pool_v), p(tables), i32(tables.shape[1]), p(npst),
+                                       i32(n), i32(n_q), i32(layer), i32(nb), p(out), i32(n_threads))
+        return out
+
+
 class Reference:
     """The reference's own headers / SYCL kernels compiled into oracle/_ref."""
 

@@ -937,6 +937,12 @@ constexpr int kCombGroups = CT / (HD / 4);
 __global__ void __launch_bounds__(CT)
 decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     const int t = blockIdx.x;
+#ifdef NOVA_DECODE_TRACE
+#define CTRACE(k) do { if (threadIdx.x == 0 && blockIdx.x < 512) g_trace[((int64_t)(a.layer & 63) * 512 + blockIdx.x) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define CTRACE(k) do {} while (0)
+#endif
+    CTRACE(5);
     int i, h;
     const int tid = threadIdx.x, g = tid / (HD / 4), q4 = tid - g * (HD / 4);
     __shared__ float s_m[kCombGroups], s_l[kCombGroups];
@@ -951,6 +957,10 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
         h = e.z >> 16;
         pt.pages = e.w;
         pt.sess = i;
+#ifdef NOVA_DECODE_TRACE
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        CTRACE(6);
+#endif
     } else {
         if (a.kv_split) {
             // single session: head kvh * G + m runs on a block whose XCD
@@ -1034,6 +1044,10 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     }
     const float inv = Lx > 0.f ? 1.f / Lx : 0.f;
     *orow = Ax * inv;
+#ifdef NOVA_DECODE_TRACE
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    CTRACE(7);
+#endif
 }
 
 // Per-step plan: block w (< split_slots) writes the record of workgroup slot w;

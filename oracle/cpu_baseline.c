@@ -111,7 +111,7 @@ static void attend(cb_geom g, const float* qv, const int64_t* lim, int nq, const
                 ls += sr[j];
             }
             l[r] = l[r] * corr + ls;
-            sr[MAX_KB - 1] = corr;            /* n <= kb < MAX_KB: slot free */
+            sr[MAX_KB - 1] = corr;            /* n <= kb <= MAX_KB - 2: slot free */
         }
         if (!any) continue;
         for (int j = 0; j < n; ++j) f16_row(vp + j * row, vf + (size_t)j * hd, hd);
@@ -216,7 +216,7 @@ void cb_attn_decode_batch(cb_geom g, const float* q, const uint16_t* pool_k, con
                           const int32_t* tables, int table_stride, const int32_t* n_keys, int n_sess,
                           int layer, int nb, float* o, int n_threads) {
     const int hd = g.hd;
-    if (g.kb > MAX_KB - 1 || hd > MAX_HD || hd % 16 || g.nh / g.nkv > 64) abort();
+    if (g.kb > MAX_KB - 2 || hd > MAX_HD || hd % 16 || g.nh / g.nkv > 64) abort();
     int n_units = 0, n_slots = 0;
     int* sess_split0 = (int*)malloc(sizeof(int) * (size_t)(n_sess + 1));
     int* sess_nsplit = (int*)malloc(sizeof(int) * (size_t)(n_sess + 1));
@@ -340,7 +340,7 @@ void cb_attn_prefill_batch(cb_geom g, const float* q, const uint16_t* pool_k, co
                            const int32_t* tables, int table_stride, const int32_t* n_past, int n_sess,
                            int n_q, int layer, int nb, float* o, int n_threads) {
     const int hd = g.hd, G = g.nh / g.nkv;
-    if (g.kb > MAX_KB - 1 || hd > MAX_HD || hd % 16 || G > 64) abort();
+    if (g.kb > MAX_KB - 2 || hd > MAX_HD || hd % 16 || G > 64) abort();
     if (n_q <= 0 || n_sess <= 0) return;
     pre_ctx c;
     c.g = g;

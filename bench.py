@@ -1056,7 +1056,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; multi-GPU figures are not produced "
-                                   "(sessions shard by GPU with no exchange -- see DESIGN.md)",
+                                   "(sessions would shard by GPU with no exchange during decode)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.workload == "decode7b":

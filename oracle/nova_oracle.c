@@ -8,7 +8,8 @@
  * Pinning (what checks each function against something other than itself):
  *   - pool, hash, registry: bit-exact against the reference's own headers
  *     compiled into oracle/_ref (tests/test_oracle_pins.py), the golden
- *     vectors of tests/kv_block_test.cpp and the SURVEY pool probe, and the
+ *     vectors of tests/kv_block_test.cpp and a pool probe (init(3, 64), two
+ *     slices, attach_prefix at 20 tokens, one COW to page 8), and the
  *     invariants of tests/cow_demo.cpp / cow_e2e_demo.cpp.
  *   - kv_store / gather / cow_copy: closed form (bit-exact copies) and a
  *     brute-force contiguous model.

@@ -309,6 +309,10 @@ __device__ __forceinline__ uint32_t swz_v(int row, int chunk) {
     return (uint32_t)(row * ROWB + ((chunk ^ (2 * (row & 7))) << 4));
 }
 
+#ifdef NOVA_PREFILL_TRACE
+__device__ uint64_t g_pf_trace[4096 * 4];
+#endif
+
 // NB: 16-column blocks per wave.  KS: key groups -- KS groups of 4 waves
 // share the workgroup's columns; group k takes the key tiles KS*i + k with
 // its own ring of tile buffers, and the groups' softmax states are merged at
@@ -342,6 +346,9 @@ prefill_kernel(PrefillArgs a) {
     const int kvh = xcd / kXcdPerHead;
     const int rank = ((int)blockIdx.x / kXcd) * kXcdPerHead + xcd % kXcdPerHead;
     if (rank >= N) return;                                  // grid padding (uniform)
+#ifdef NOVA_PREFILL_TRACE
+    const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
+#endif
     int item;
     if (a.n_sess == 1 || N > kRankMax) item = (rank / n_cg) * n_cg + (n_cg - 1 - rank % n_cg);
     else item = lpt_item<NT>(a, rank, n_cg, n_cols, COLS_WG, reinterpret_cast<int*>(&s_kv[0][0][0]));
@@ -731,6 +738,23 @@ prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) *reinterpret_cast<f4*>(op + 16 * cb + 4 * g) = acc[b][cb] * inv;
     }
+#ifdef NOVA_PREFILL_TRACE
+    // development builds: per-workgroup start, end, hardware ids and key tiles
+    if constexpr (KS == 1) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0 && blockIdx.x < 4096) {
+            unsigned hw, xcc;
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
+            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+            uint64_t* tr = g_pf_trace + (int64_t)blockIdx.x * 4;
+            tr[0] = t_start;
+            tr[1] = __builtin_amdgcn_s_memrealtime();
+            tr[2] = hw;
+            tr[3] = ((uint64_t)xcc << 32) | (uint32_t)n_tiles;
+        }
+    }
+#endif
 }
 
 int compute_units() {
@@ -782,6 +806,10 @@ void launch(const PrefillArgs& a, int n_sess, hipStream_t s) {
 using namespace nova;
 
 extern "C" {
+
+#ifdef NOVA_PREFILL_TRACE
+void nova_prefill_trace_copy(void* host) { NOVA_HIP(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_pf_trace), sizeof(g_pf_trace))); }
+#endif
 
 void launch_attn_prefill_paged(const float* q, const uint16_t* pool_k, const uint16_t* pool_v,
                                const int32_t* table, int layer, int nb, int n_q, int n_past, float* o,

@@ -105,3 +105,29 @@ def test_noalloc_decode_rejects_sizes_beyond_its_workspace(n_sess):
                    f"n.launch_attn_decode_paged_batch_noalloc(1, 1, 1, 1, 4, 1, {n_sess}, 0, 4, None, None, 1, None)")
     assert r.returncode != 0
     assert "static workspace" in r.stderr and f"n_sess {n_sess}" in r.stderr, r.stderr[-500:]
+
+
+def _consumer():
+    exe = Path(__file__).resolve().parent / "cpp" / "abi_consumer"
+    if not exe.exists():
+        pytest.skip("tests/cpp/abi_consumer is not built (build() makes it)")
+    return exe
+
+
+def test_cpp_consumer_builds_and_loads():
+    """tests/cpp/abi_consumer.cpp compiles against the public headers alone
+    (built by build()) and links and loads the 1.5B library; without a GPU it
+    reports the skip code 77 before touching the device."""
+    r = subprocess.run([str(_consumer())], capture_output=True, text=True, timeout=120)
+    assert r.returncode in (0, 77), r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+def test_cpp_consumer_on_gpu():
+    """The C++ caller drives a fork, a COW, appends and decodes through the C
+    ABI exactly as the reference's engine would, and checks its own results."""
+    print("[case] tests/cpp/abi_consumer", flush=True)
+    r = subprocess.run([str(_consumer())], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "abi_consumer: PASS" in r.stdout

@@ -7,10 +7,12 @@
 // launch_kv_store_paged; session B forks A's first 99 tokens (attach_prefix,
 // unaligned, so the tail page is shared), runs session_cow over position 99
 // and appends its own token 99; both sessions then decode with
-// launch_attn_decode_paged.  Checks: the appended rows read back bit-exact,
-// one COW with the donor page untouched and the refcounts of the shared and
-// copied pages, and both decode outputs against an f64 softmax computed
-// here, within max-abs 2e-3 / rel 1e-2.  Exit 0 = pass, 77 = no GPU.
+// launch_attn_decode_paged, and A's last 20 positions run as a chunked
+// prefill through launch_attn_prefill_paged.  Checks: the appended rows read
+// back bit-exact, one COW with the donor page untouched and the refcounts of
+// the shared and copied pages, and the decode and prefill outputs against an
+// f64 softmax computed here, within max-abs 2e-3 / rel 1e-2.
+// Exit 0 = pass, 77 = no GPU.
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -169,6 +171,49 @@ int main() {
         }
         std::printf("session %d: decode max |gpu - f64| = %.3e\n", s, worst);
         check(ok, s == a ? "decode of the donor session" : "decode of the forked session");
+    }
+
+    // chunked prefill through the reference signature: A's last 20 positions
+    // as queries over its own keys, causal (query i sees keys 0..80+i)
+    {
+        const int n_q = 20, n_past = n_tok - n_q;
+        std::vector<float> qs((size_t)n_q * g.nh * g.hd);
+        for (auto& x : qs) x = nd(rng);
+        float* dqs = static_cast<float*>(dev_alloc(qs.size() * 4));
+        float* dos = static_cast<float*>(dev_alloc(qs.size() * 4));
+        dev_upload(dqs, qs.data(), qs.size() * 4);
+        launch_attn_prefill_paged(dqs, pk, pv, nova_paged_table_dev(pg, a), layer, nb, n_q, n_past, dos, st);
+        dev_stream_sync(st);
+        std::vector<float> os(qs.size());
+        dev_download(os.data(), dos, os.size() * 4);
+        double worst = 0.0;
+        bool ok = true;
+        for (int i = 0; i < n_q; ++i)
+            for (int h = 0; h < g.nh; ++h) {
+                const int kvh = h / G, n_keys = n_past + i + 1;
+                const float* qr = &qs[((size_t)i * g.nh + h) * g.hd];
+                std::vector<double> sc(n_keys);
+                double mx = -1e300, den = 0.0;
+                for (int t = 0; t < n_keys; ++t) {
+                    const uint16_t* kr = at(hk, tab_a, t) + (size_t)kvh * g.hd;
+                    double acc = 0.0;
+                    for (int e = 0; e < g.hd; ++e) acc += (double)qr[e] * half_value(kr[e]);
+                    sc[t] = acc * scale;
+                    mx = std::fmax(mx, sc[t]);
+                }
+                for (auto& x : sc) den += (x = std::exp(x - mx));
+                for (int e = 0; e < g.hd; ++e) {
+                    double num = 0.0;
+                    for (int t = 0; t < n_keys; ++t) num += sc[t] * half_value(at(hv, tab_a, t)[(size_t)kvh * g.hd + e]);
+                    const double ref = num / den, got = os[((size_t)i * g.nh + h) * g.hd + e];
+                    worst = std::fmax(worst, std::fabs(got - ref));
+                    ok &= std::isfinite(got) && std::fabs(got - ref) <= 2e-3 + 1e-2 * std::fabs(ref);
+                }
+            }
+        std::printf("prefill of %d queries: max |gpu - f64| = %.3e\n", n_q, worst);
+        check(ok, "chunked prefill of the donor session");
+        dev_free(dqs);
+        dev_free(dos);
     }
 
     for (void* p : {(void*)dka, (void*)dva, (void*)dkb, (void*)dvb, (void*)dq, (void*)dout, (void*)scratch}) dev_free(p);

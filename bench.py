@@ -73,6 +73,9 @@ def parse():
     ap.add_argument("--main-only", action="store_true",
                     help="decode workloads: time the batched step only (no per-session or fused-RoPE comparison legs)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="0 = all host cores")
+    ap.add_argument("--configs", default="all", choices=["all", "main"],
+                    help="decode7b: 'all' adds configs 1, 3, 4 and 5 (their own timing, roofline, CPU baseline "
+                         "and parity) under the line's 'configs' key; 'main' times config 2 only")
     return ap.parse_args()
 
 
@@ -203,8 +206,23 @@ class DecodeWorkload:
             nv.testkit_decode_stream_floor(self.k.ptr, self.v.ptr, self.tables.ptr, self.max_pages, self.n, l,
                                            self.nb, self.ws.ptr, s)
 
+        # contiguous floor: the layer's algorithmic bytes as one contiguous
+        # non-temporal read by one 512-thread workgroup per CU (no pages, no
+        # table); layers take disjoint ranges (K pool for the first half of
+        # the layers, V pool for the rest), so nothing is read twice per step
+        half = (L + 1) // 2
+        nbytes = min(self.bytes_per_step() // L, nv.n_layers * self.layer_halves * 2 // half) // 16 * 16
+        self.contig_bytes = nbytes
+        cus = nv.dev_cu_count()
+        sink = nv.alloc(cus * 512 * 4)
+
+        def contig(l):
+            src = (self.k.ptr if l < half else self.v.ptr) + (l % half) * nbytes
+            nv.testkit_stream_read(src, nbytes, cus, sink.ptr, s)
+
         out = {}
-        for name, fn in (("pair", self.launch_layer), ("split", split_only), ("floor", floor)):
+        for name, fn in (("pair", self.launch_layer), ("split", split_only), ("floor", floor),
+                         ("contig", contig)):
             nv.dev_graph_begin(s)
             for l in range(L):
                 fn(l)
@@ -217,7 +235,7 @@ class DecodeWorkload:
                 nv.dev_graph_launch(g, s)
             out[name] = t.stop() / (reps * L)
             nv.dev_graph_destroy(g)
-        return out["pair"], out["split"], out["floor"]
+        return out["pair"], out["split"], out["floor"], out["contig"]
 
     def per_session_ms(self, steps, warmup):
         """The reference's call pattern for the same step (Engine::decode_batch,
@@ -364,24 +382,29 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
     nova.dev_sync()
     bytes_step = wl.bytes_per_step()
     gbs = bytes_step / (ms * 1e-3) / 1e9
-    pair_ms, split_ms, floor_ms = wl.kernel_times()
+    pair_ms, split_ms, floor_ms, contig_ms = wl.kernel_times()
     bytes_launch = bytes_step / wl.layers
     split_gbs = bytes_launch / (split_ms * 1e-3) / 1e9
     pair_gbs = bytes_launch / (pair_ms * 1e-3) / 1e9
     traffic = load_traffic(workload_name)
     roof = {"bound": "hbm", "achieved": round(split_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(split_gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "decode_split_kernel (one layer of all sessions)",
+            "kernel": "decode_split_kernel alone (one layer of all sessions; the split + combine pair "
+                      "that callers run is launch_pair_*)",
             "kernel_us": round(split_ms * 1e3, 2), "bytes_per_launch": bytes_launch,
             "launch_pair_us": round(pair_ms * 1e3, 2),
             "launch_pair_frac": round(pair_gbs / HBM_PEAK_GBS, 4),
             "step_frac": round(gbs / HBM_PEAK_GBS, 4),
             "stream_floor_us": round(floor_ms * 1e3, 2),
             "stream_floor_frac": round(bytes_launch / (floor_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "contig_floor_us": round(contig_ms * 1e3, 2),
+            "contig_floor_frac": round(wl.contig_bytes / (contig_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "contig_floor_bytes": wl.contig_bytes,
             "timing": "HIP events around graph replays of the 28 layers' launches: split kernel alone "
                       "(testkit_attn_decode_split_only), the split + combine pair "
                       "(launch_attn_decode_paged_planned) and the stream floor (testkit_decode_stream_floor: "
-                      "the split grid reading the same pages with the same loads, no arithmetic); "
+                      "the split grid reading the same pages with the same loads, no arithmetic), the contiguous "
+                      "floor (testkit_stream_read: the same bytes as one contiguous read, one workgroup per CU); "
                       "step_frac = the timed step incl. the plan kernel"}
     cpu = None
     parity = None
@@ -623,15 +646,20 @@ def run_cow(args):
                                "(unaligned, so the half-filled tail page is shared), suffix U[0,1024] "
                                "appended token by token", "fork_tokens": FORK, "children": n_child,
                    "suffix_tokens_total": int(suffix.sum())},
-        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": load_traffic("cow"),
-                     "kernel": "cow_apply_kernel (launch_kv_cow_apply)", "kernel_us": round(cow_ms * 1e3, 2),
-                     "bytes_per_launch": cow_bytes},
-        "distinct_donors": {"us": round(distinct_ms * 1e3, 2),
-                            "GBs": round(cow_bytes / (distinct_ms * 1e-3) / 1e9, 1),
-                            "frac": round(cow_bytes / (distinct_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                            "what": "the same 64-copy launch with 64 distinct donor pages (no cache reuse): "
-                                    "the kernel's HBM rate"},
+        # the roofline is the kernel's HBM rate: the same 64-copy launch with 64
+        # distinct donor pages, every byte from HBM.  Config 3's own launch
+        # copies 4 donor pages 16 times each; its reads come from cache, so its
+        # rate (shared_donors) exceeds the HBM peak and is no HBM figure.
+        "roofline": {"bound": "hbm", "achieved": round(cow_bytes / (distinct_ms * 1e-3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(cow_bytes / (distinct_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "cow_apply_kernel (launch_kv_cow_apply), 64 copies from 64 distinct donor pages",
+                     "kernel_us": round(distinct_ms * 1e3, 2), "bytes_per_launch": cow_bytes},
+        "shared_donors": {"us": round(cow_ms * 1e3, 2), "GBs": round(gbs, 1),
+                          "traffic": load_traffic("cow"),
+                          "what": "config 3's own launch: 64 copies of 4 donor pages (16 children per donor), "
+                                  "the donor reads served from cache; traffic = measured HBM bytes per launch"},
         "first_cow_batch_us": round(first_ms * 1e3, 2),
         "append_ms_total": round(append_ms, 1), "append_steps": maxL,
         "parity": {"tables": tables_ok, "device_tables": dev_ok, "refcounts": refcnt_ok, "free_list": free_ok,
@@ -1052,6 +1080,47 @@ def run_copycal(args):
             "bytes_read_per_launch": nbytes, "bytes_written_per_launch": nbytes, "kernel_us": round(ms * 1e3, 2)}
 
 
+def single1p5b_cfg():
+    return np.array([1024], np.int32), {
+        "metric": "paged decode step, Qwen2.5-1.5B single session",
+        "config": {"workload": "config1: 1 session ctx 1024, Qwen2.5-1.5B attention (12q/2kv, 28 layers)",
+                   "sessions": 1, "ctx": 1024, "layers": 28}}
+
+
+def longctx14b_cfg():
+    return np.full(8, 32767, np.int32), {
+        "metric": "paged flash-decode KV GB/s, Qwen2.5-14B long context",
+        "config": {"workload": "config4: 8 sessions x 32768 tokens, Qwen2.5-14B attention "
+                               "(40q/8kv, hd128, 48 layers), ~51.5 GB KV resident",
+                   "sessions": 8, "ctx": 32768, "layers": 48}}
+
+
+# keys of a workload's line that the configs sub-objects leave out (the top
+# level states them once)
+_SUB_DROP = ("n_gpus", "steps", "warmup", "higher_is_better", "scaling", "vs_baseline", "data")
+
+
+def other_configs(args):
+    """Configs 1, 3, 4 and 5 of BASELINE.json, each with its own timing,
+    roofline, CPU baseline and parity, for the default line (config 2 is the
+    line itself).  Decode configs time the batched step only."""
+    import copy
+    sub = copy.copy(args)
+    sub.main_only = True
+    out = {}
+    legs = [("config1", lambda: run_decode(sub, "qwen25_1p5b", single1p5b_cfg()[0], "single1p5b",
+                                           single1p5b_cfg()[1], "Qwen2.5-1.5B, 1 session")),
+            ("config3", lambda: run_cow(sub)),
+            ("config4", lambda: run_decode(sub, "qwen25_14b", longctx14b_cfg()[0], "longctx14b",
+                                           longctx14b_cfg()[1], "Qwen2.5-14B, 8 x 32K")),
+            ("config5", lambda: run_prefill(sub))]
+    for name, fn in legs:
+        print(f"[leg] {name}", file=sys.stderr, flush=True)
+        r = fn()
+        out[name] = {k: v for k, v in r.items() if k not in _SUB_DROP}
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -1067,18 +1136,13 @@ def main():
                                       "16 sessions ctx U[512,8192], 1-token append + split-K attention per layer",
                           "sessions": 16, "ctx": ctx.tolist(), "layers": 28, "page_tokens": 16}}
         line = run_decode(args, "qwen25_7b", ctx, "decode7b", cfg, "Qwen2.5-7B, 16 sessions")
+        if args.configs == "all":
+            line["configs"] = other_configs(args)
     elif args.workload == "longctx14b":
-        ctx = np.full(8, 32767, np.int32)
-        cfg = {"metric": "paged flash-decode KV GB/s, Qwen2.5-14B long context",
-               "config": {"workload": "config4: 8 sessions x 32768 tokens, Qwen2.5-14B attention "
-                                      "(40q/8kv, hd128, 48 layers), ~51.5 GB KV resident",
-                          "sessions": 8, "ctx": 32768, "layers": 48}}
+        ctx, cfg = longctx14b_cfg()
         line = run_decode(args, "qwen25_14b", ctx, "longctx14b", cfg, "Qwen2.5-14B, 8 x 32K")
     elif args.workload == "single1p5b":
-        ctx = np.array([1024], np.int32)
-        cfg = {"metric": "paged decode step, Qwen2.5-1.5B single session",
-               "config": {"workload": "config1: 1 session ctx 1024, Qwen2.5-1.5B attention (12q/2kv, 28 layers)",
-                          "sessions": 1, "ctx": 1024, "layers": 28}}
+        ctx, cfg = single1p5b_cfg()
         line = run_decode(args, "qwen25_1p5b", ctx, "single1p5b", cfg, "Qwen2.5-1.5B, 1 session")
     elif args.workload == "copycal":
         line = run_copycal(args)

@@ -37,7 +37,13 @@ HIP_SOURCES = [
     "code/kernel/hip/kv_pages.hip",
     "code/kernel/hip/rope.hip",
     "code/kernel/hip/q4k.hip",
-    "code/kernel/hip/testkit.hip",
+]
+# the test kit library libnova_testkit_<model>.so (testkit/nova_testkit.h):
+# synthetic fills, calibration kernels, and the decode kernels' test entry
+# points compiled from the product source with -DNOVA_TESTKIT
+TESTKIT_SOURCES = [
+    ("testkit/testkit.hip", []),
+    ("code/kernel/hip/attn_decode.hip", ["-DNOVA_TESTKIT"]),
 ]
 CXX_SOURCES = [
     "code/capi/graph_capi.cpp",
@@ -46,7 +52,7 @@ CXX_SOURCES = [
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 COMMON = [
     "-std=c++17", "-O3", "-fPIC", "-Wall", "-Wno-unused-function",
-    f"-I{ROOT / 'include'}", f"-I{PKG / 'code'}", f"-I{PKG / 'code/kernel/hip'}",
+    f"-I{ROOT / 'include'}", f"-I{PKG / 'code'}", f"-I{PKG / 'code/kernel/hip'}", f"-I{PKG / 'testkit'}",
 ]
 HIP_FLAGS = [
     "--offload-arch=gfx950",
@@ -63,12 +69,12 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed: {cmd[-1]}")
 
 
-def _compile(src: str, model: str, define: str) -> Path:
-    out = OBJ / model / (Path(src).stem + ".o")
+def _compile(src: str, model: str, define: str, extra: tuple = (), sub: str = "") -> Path:
+    out = OBJ / model / sub / (Path(src).stem + ".o")
     out.parent.mkdir(parents=True, exist_ok=True)
     path = PKG / src
     if src.endswith(".hip"):
-        cmd = [HIPCC, *COMMON, *HIP_FLAGS, f"-D{define}", "-c", str(path), "-o", str(out)]
+        cmd = [HIPCC, *COMMON, *HIP_FLAGS, f"-D{define}", *extra, "-c", str(path), "-o", str(out)]
     else:
         cmd = [HIPCC, *COMMON, f"-D{define}", "-x", "c++", "-c", str(path), "-o", str(out)]
     _run(cmd)
@@ -85,17 +91,20 @@ def build(models: list[str] | None = None, jobs: int | None = None) -> list[Path
         for name in names:
             define = MODELS[name]
             for src in HIP_SOURCES + CXX_SOURCES:
-                futs[ex.submit(_compile, src, name, define)] = name
-        objs: dict[str, list[Path]] = {n: [] for n in names}
+                futs[ex.submit(_compile, src, name, define)] = (name, "hip")
+            for src, extra in TESTKIT_SOURCES:
+                futs[ex.submit(_compile, src, name, define, tuple(extra), "testkit")] = (name, "testkit")
+        objs: dict[tuple, list[Path]] = {}
         for f in cf.as_completed(futs):
-            objs[futs[f]].append(f.result())
+            objs.setdefault(futs[f], []).append(f.result())
     for name in names:
-        out = LIB / f"libnova_hip_{name}.so"
-        tmp = out.with_suffix(".so.tmp")
-        _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp),
-              *sorted(map(str, objs[name])), "-lpthread"])
-        os.replace(tmp, out)
-        built.append(out)
+        for kind in ("hip", "testkit"):
+            out = LIB / f"libnova_{kind}_{name}.so"
+            tmp = out.with_suffix(".so.tmp")
+            _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp),
+                  *sorted(map(str, objs[(name, kind)])), "-lpthread"])
+            os.replace(tmp, out)
+            built.append(out)
     return built
 
 

@@ -69,6 +69,9 @@
 #include "check.h"
 #include "model.h"
 #include "nova_kernel.h"
+#ifdef NOVA_TESTKIT
+#include "nova_testkit.h"
+#endif
 #include "rope_math.h"
 
 namespace nova {
@@ -114,7 +117,18 @@ struct DecodeArgs {
     int gw;                  // workgroups in the grid
     int wave_parts;          // 1: a partial slot per (workgroup, wave row), no in-workgroup merge
     int kv_split;            // 1: grid.y = kv head, all waves of a workgroup on that head (no fused append)
+    int spin;                // polls of the in-workgroup exchange before it gives up (kSpinLimit)
+    int32_t* status;         // batched path: the plan's status word (null: none)
 };
+
+// Bound of the LDS-flag wait in the one-slot partial exchange.  The partner
+// wave of a kv head always arrives (every wave of the workgroup reaches the
+// exchange), so the bound only guards against a hang; if it ever runs out,
+// the keeper sets kStatusExchange in the plan's status word and writes NaN
+// into its partial row, so the affected heads come out NaN, never silently
+// wrong.
+constexpr int kSpinLimit = 1 << 22;
+constexpr int32_t kStatusExchange = 1;
 
 // Per-step plan, written once per decode step by decode_plan_kernel (n_keys
 // and block tables are the same for every layer of a step):
@@ -146,9 +160,12 @@ __host__ __device__ __forceinline__ int logical_of(int w, int stride, int gw) {
 // plan: [session table n_sess x 4 | combine map n_sess*NH x {kc, k, sess | head << 16, pages} | records]
 __host__ __device__ constexpr int64_t plan_map_off(int n_sess) { return (int64_t)n_sess * 4; }
 __host__ __device__ constexpr int64_t plan_rec_off(int n_sess) { return (int64_t)n_sess * 4 + (int64_t)n_sess * NH * 4; }
-__host__ __device__ constexpr int64_t plan_ints(int n_sess, int gw) {
+// one status word after the records: cleared by every plan launch, OR-ed
+// with kStatus* by the kernels of the step's layers
+__host__ __device__ constexpr int64_t plan_status_off(int n_sess, int gw) {
     return plan_rec_off(n_sess) + (int64_t)split_slots(n_sess, gw) * kRec;
 }
+__host__ __device__ constexpr int64_t plan_ints(int n_sess, int gw) { return plan_status_off(n_sess, gw) + 1; }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(v, m, 64); }
 
@@ -185,6 +202,15 @@ __host__ __device__ __forceinline__ int share_of(int T, int gw) {
     const int even = (T + gw - 1) / gw;
     return even > kMinShare ? even : kMinShare;
 }
+
+// Page range of workgroup j of a session with `pages` pages split over k
+// workgroups: [j*pages/k, (j+1)*pages/k).  The plan kernel, the in-kernel
+// partition and the combine's row count all take it from here, so a range
+// never exceeds range_max_pages(pages, k).
+__host__ __device__ __forceinline__ int range_begin(int j, int pages, int k) {
+    return (int)((int64_t)j * pages / k);
+}
+__host__ __device__ __forceinline__ int range_max_pages(int pages, int k) { return (pages + k - 1) / k; }
 
 // The batch partition, derived by one wave from n_keys (every wave that needs
 // it computes it; no LDS, no barrier).  P_i = pages of session i, T = sum P_i,
@@ -371,8 +397,8 @@ decode_split_kernel(DecodeArgs a) {
         i = pt.sess;
         n_keys = pt.n_keys;
         const int j = w - pt.kc;                 // this workgroup's share of session i
-        pa = (int)((int64_t)j * pt.pages / pt.k);
-        pb = (int)((int64_t)(j + 1) * pt.pages / pt.k);
+        pa = range_begin(j, pt.pages, pt.k);
+        pb = range_begin(j + 1, pt.pages, pt.k);
         tv = (pa + lane < pb) ? a.tables[(int64_t)i * a.table_stride + pa + lane] : 0;
     }
     // settle the slice register here (one wait, nothing else in flight yet):
@@ -741,16 +767,24 @@ decode_split_kernel(DecodeArgs a) {
             // slowest wave of the workgroup); bounded wait, every wave of the
             // workgroup reaches this point
             if (lane == 0) __hip_atomic_store(&s_ready[wave], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+            bool gave_up = false;
 #pragma unroll
             for (int rr = 0; rr < R; ++rr) {
                 const int ww = kvh + NKV * rr;
                 if (ww == wave) continue;
-                for (int it = 0; it < (1 << 22); ++it) {
+                bool seen = false;
+                for (int it = 0; it < a.spin; ++it) {
                     const int f = __hip_atomic_load(&s_ready[ww], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    if (__builtin_amdgcn_readfirstlane(f)) break;
+                    if (__builtin_amdgcn_readfirstlane(f)) {
+                        seen = true;
+                        break;
+                    }
                     __builtin_amdgcn_s_sleep(1);
                 }
+                gave_up |= !seen;
             }
+            if (gave_up && keeper == r && lane == 0 && a.status)
+                __hip_atomic_fetch_or(a.status, kStatusExchange, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (keeper == r && c < G) {
                 float M = -INFINITY;
 #pragma unroll
@@ -785,6 +819,14 @@ decode_split_kernel(DecodeArgs a) {
                     }
                 }
                 float* row = a.part + ((int64_t)slot * NH + kvh * G + c) * PW;
+                if (gave_up) {
+                    // the partner's rows may not be in LDS: poison this slot so
+                    // that the combine's output for these heads is NaN
+                    M = 0.f;
+                    L = 1.f;
+#pragma unroll
+                    for (int cb = 0; cb < 8; ++cb) A[cb] = f4{NAN, NAN, NAN, NAN};
+                }
                 if (g == 0) {
                     row[0] = M;
                     row[1] = L;
@@ -859,6 +901,7 @@ decode_split_kernel(DecodeArgs a) {
 #endif
 }
 
+#ifdef NOVA_TESTKIT
 // Stream floor (test kit): the planned split grid reading exactly the split
 // kernel's bytes -- the same plan records, page pairs per wave row, lane
 // offsets and non-temporal 16-byte loads -- with no arithmetic but a running
@@ -920,6 +963,8 @@ decode_stream_floor_kernel(DecodeArgs a) {
     }
     reinterpret_cast<uint32_t*>(a.part)[(int64_t)w * THREADS + tid] = sum[0] + sum[1] + sum[2] + sum[3];
 }
+
+#endif  // NOVA_TESTKIT
 
 // Combine: one workgroup per (session, head) merges the session's k_i
 // partials (slots kc_i .. kc_i+k_i-1) with the rule of fa_combine_kernel
@@ -989,7 +1034,7 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     // ceil(pages / k) pages; rows past its pairs hold l = 0): config 1 reads
     // 34 rows in one round instead of 68 in two
     const int stride = a.wave_parts == 1 ? R : 1;
-    const int used = a.wave_parts == 1 ? min(R, ((pt.pages + pt.k - 1) / pt.k + 1) >> 1) : 1;
+    const int used = a.wave_parts == 1 ? min(R, (range_max_pages(pt.pages, pt.k) + 1) >> 1) : 1;
     const int n_rows = pt.k * used;
     const float* base = a.part + (int64_t)pt.kc * stride * SEG + (int64_t)h * PW;
     float M = -INFINITY, L = 0.f;
@@ -1058,6 +1103,7 @@ decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
     const int w = blockIdx.x, lane = threadIdx.x;
     const int n_slots = split_slots(a.n_sess, a.gw);
     if (w == n_slots) {
+        if (lane == 0) plan[plan_status_off(a.n_sess, a.gw)] = 0;
         __shared__ int s_kc[kMaxBatch], s_k[kMaxBatch], s_mid[kMaxBatch], s_home[kMaxBatch], s_rank[kMaxBatch],
             s_pg[kMaxBatch];
         // session table: the same prefix as partition(), one lane per session
@@ -1155,8 +1201,8 @@ decode_plan_kernel(DecodeArgs a, int32_t* __restrict__ plan) {
         return;
     }
     const int j = L - pt.kc;
-    const int pa = (int)((int64_t)j * pt.pages / pt.k);
-    const int pb = (int)((int64_t)(j + 1) * pt.pages / pt.k);
+    const int pa = range_begin(j, pt.pages, pt.k);
+    const int pb = range_begin(j + 1, pt.pages, pt.k);
     rec[lane] = pa + lane < pb ? a.tables[(int64_t)pt.sess * a.table_stride + pa + lane] : 0;
     if (lane < 5) {
         const int v = lane == 0 ? pt.sess : lane == 1 ? pa : lane == 2 ? pb : lane == 3 ? pt.n_keys : L;
@@ -1209,6 +1255,8 @@ DecodeArgs batch_args(const int32_t* tables, int table_stride, const int32_t* n_
     a.gw = batch_workgroups();
     a.plan = static_cast<const int32_t*>(workspace);
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan_bytes(n_sess));
+    a.spin = kSpinLimit;
+    a.status = static_cast<int32_t*>(workspace) + plan_status_off(n_sess, a.gw);
     // Partial slots: with two waves per kv head (7B) they merge through LDS
     // into one slot per workgroup (half the partial bytes, same step time);
     // with four (1.5B) the exchange costs more than it saves: one slot per
@@ -1220,6 +1268,7 @@ DecodeArgs batch_args(const int32_t* tables, int table_stride, const int32_t* n_
     return a;
 }
 
+#ifndef NOVA_TESTKIT
 // ---- workspace without allocation: a file-scope device array ----
 // For callers that cannot allocate (code under graph capture, serving loops,
 // harnesses that forbid hipMalloc): the batched decode with its plan and
@@ -1254,6 +1303,8 @@ void* scratch_address() {
     return ptr[dev];
 }
 
+#endif  // !NOVA_TESTKIT
+
 }  // namespace
 }  // namespace nova
 
@@ -1264,6 +1315,8 @@ extern "C" {
 #ifdef NOVA_DECODE_TRACE
 void nova_decode_trace_copy(void* host) { NOVA_HIP(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), sizeof(g_trace))); }
 #endif
+
+#ifndef NOVA_TESTKIT
 
 size_t attn_decode_batch_workspace_bytes(int n_sess) {
     NOVA_REQUIRE(n_sess >= 1 && n_sess <= kMaxBatch);
@@ -1295,38 +1348,6 @@ void launch_attn_decode_paged_planned(const float* q, uint16_t* pool_k, uint16_t
     a.k_new = k_new;
     a.v_new = v_new;
     launch_pair(a, n_sess, o, reinterpret_cast<hipStream_t>(s));
-}
-
-void testkit_attn_decode_split_only(const float* q, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
-                                    int table_stride, int n_sess, int layer, int nb, const uint16_t* k_new,
-                                    const uint16_t* v_new, void* workspace, nova_stream_t s) {
-    NOVA_REQUIRE(q && pool_k && pool_v);
-    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0);
-    NOVA_REQUIRE((k_new == nullptr) == (v_new == nullptr));
-    DecodeArgs a = batch_args(tables, table_stride, nullptr, n_sess, workspace);
-    a.q = q;
-    a.pool_k = pool_k;
-    a.pool_v = pool_v;
-    a.layer = layer;
-    a.nb = nb;
-    a.k_new = k_new;
-    a.v_new = v_new;
-    launch_split(a, n_sess, reinterpret_cast<hipStream_t>(s));
-}
-
-void testkit_decode_stream_floor(const uint16_t* pool_k, const uint16_t* pool_v, const int32_t* tables,
-                                 int table_stride, int n_sess, int layer, int nb, void* workspace, nova_stream_t s) {
-    NOVA_REQUIRE(pool_k && pool_v);
-    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0);
-    DecodeArgs a = batch_args(tables, table_stride, nullptr, n_sess, workspace);
-    a.pool_k = pool_k;
-    a.pool_v = pool_v;
-    a.layer = layer;
-    a.nb = nb;
-    static_assert(THREADS <= R * NH * PW, "one sink word per thread fits in a workgroup's partial slots");
-    hipLaunchKernelGGL(decode_stream_floor_kernel, dim3(split_slots(n_sess, a.gw)), dim3(THREADS), 0,
-                       reinterpret_cast<hipStream_t>(s), a);
-    NOVA_LAUNCHED();
 }
 
 void launch_attn_decode_paged_rope_planned(const float* q, const float* k_new, const float* v_new, const float* cs,
@@ -1415,7 +1436,75 @@ void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint
     a.part = scratch;
     a.gw = gw;
     a.kv_split = 1;   // NKV workgroups per partial slot: 31 * NKV CUs per call
+    a.spin = kSpinLimit;
     launch_pair(a, 1, o, reinterpret_cast<hipStream_t>(s));
 }
+
+int attn_decode_batch_status(const void* workspace, int n_sess) {
+    NOVA_REQUIRE(workspace && n_sess >= 1 && n_sess <= kMaxBatch);
+    int32_t v = 0;
+    NOVA_HIP(hipDeviceSynchronize());
+    NOVA_HIP(hipMemcpy(&v, static_cast<const int32_t*>(workspace) + plan_status_off(n_sess, batch_workgroups()),
+                       sizeof(v), hipMemcpyDeviceToHost));
+    return v;
+}
+
+#endif  // !NOVA_TESTKIT
+
+#ifdef NOVA_TESTKIT
+
+void testkit_attn_decode_split_only(const float* q, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
+                                    int table_stride, int n_sess, int layer, int nb, const uint16_t* k_new,
+                                    const uint16_t* v_new, void* workspace, nova_stream_t s) {
+    NOVA_REQUIRE(q && pool_k && pool_v);
+    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0);
+    NOVA_REQUIRE((k_new == nullptr) == (v_new == nullptr));
+    DecodeArgs a = batch_args(tables, table_stride, nullptr, n_sess, workspace);
+    a.q = q;
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.layer = layer;
+    a.nb = nb;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    launch_split(a, n_sess, reinterpret_cast<hipStream_t>(s));
+}
+
+void testkit_decode_stream_floor(const uint16_t* pool_k, const uint16_t* pool_v, const int32_t* tables,
+                                 int table_stride, int n_sess, int layer, int nb, void* workspace, nova_stream_t s) {
+    NOVA_REQUIRE(pool_k && pool_v);
+    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0);
+    DecodeArgs a = batch_args(tables, table_stride, nullptr, n_sess, workspace);
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.layer = layer;
+    a.nb = nb;
+    static_assert(THREADS <= R * NH * PW, "one sink word per thread fits in a workgroup's partial slots");
+    hipLaunchKernelGGL(decode_stream_floor_kernel, dim3(split_slots(n_sess, a.gw)), dim3(THREADS), 0,
+                       reinterpret_cast<hipStream_t>(s), a);
+    NOVA_LAUNCHED();
+}
+
+
+void testkit_attn_decode_planned_spin(const float* q, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
+                                      int table_stride, int n_sess, int layer, int nb, const uint16_t* k_new,
+                                      const uint16_t* v_new, float* o, void* workspace, int spin_limit,
+                                      nova_stream_t s) {
+    NOVA_REQUIRE(q && pool_k && pool_v && o && spin_limit >= 0);
+    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0);
+    NOVA_REQUIRE((k_new == nullptr) == (v_new == nullptr));
+    DecodeArgs a = batch_args(tables, table_stride, nullptr, n_sess, workspace);
+    a.q = q;
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.layer = layer;
+    a.nb = nb;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.spin = spin_limit;
+    launch_pair(a, n_sess, o, reinterpret_cast<hipStream_t>(s));
+}
+
+#endif  // NOVA_TESTKIT
 
 }  // extern "C"

@@ -73,8 +73,7 @@ _SIGS = {
     "launch_attn_decode_paged_rope_batch": (None, [vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp]),
     "launch_attn_decode_paged_batch": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp, vp, vp]),
     "launch_attn_decode_paged_batch_noalloc": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp, vp]),
-    "testkit_attn_decode_split_only": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp]),
-    "testkit_decode_stream_floor": (None, [vp, vp, vp, i32, i32, i32, i32, vp, vp]),
+    "attn_decode_batch_status": (i32, [vp, i32]),
     "launch_attn_decode_plan": (None, [vp, i32, vp, i32, vp, vp]),
     "launch_attn_decode_paged_planned": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]),
     "launch_attn_prefill_paged_batch": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, i32, vp, vp]),
@@ -93,8 +92,6 @@ _SIGS = {
     "launch_kv_cow_apply": (None, [vp, vp, i32, vp, C.POINTER(CowOp), i32, vp]),
     "launch_kv_zero_pages": (None, [vp, vp, i32, vp, i32, vp]),
     "launch_table_patch": (None, [vp, vp, vp, i32, vp]),
-    "testkit_fill_normal_f16": (None, [vp, u64, u64, f32, vp]),
-    "testkit_copy": (None, [vp, vp, u64, vp]),
     # nova_graph.h
     "nova_kvpool_new": (vp, [i32, i64]),
     "nova_kvpool_delete": (None, [vp]),
@@ -150,9 +147,24 @@ _SIGS = {
     "nova_paged_table_dev": (vp, [vp, i32]),
 }
 
+# test kit library (conflux-nova_amd/testkit/nova_testkit.h): not part of the
+# product; bound onto the same handle when it is built
+_TESTKIT_SIGS = {
+    "testkit_fill_normal_f16": (None, [vp, u64, u64, f32, vp]),
+    "testkit_copy": (None, [vp, vp, u64, vp]),
+    "testkit_stream_read": (None, [vp, u64, i32, vp, vp]),
+    "testkit_attn_decode_split_only": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp]),
+    "testkit_decode_stream_floor": (None, [vp, vp, vp, i32, i32, i32, i32, vp, vp]),
+    "testkit_attn_decode_planned_spin": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, i32, vp]),
+}
+
 
 def lib_path(model: str) -> Path:
     return LIB_DIR / f"libnova_hip_{model}.so"
+
+
+def testkit_path(model: str) -> Path:
+    return LIB_DIR / f"libnova_testkit_{model}.so"
 
 
 class Nova:
@@ -171,6 +183,14 @@ class Nova:
             fn.restype = res
             fn.argtypes = args
             setattr(self, name, fn)
+        tk = testkit_path(model)
+        self.testkit = C.CDLL(str(tk), mode=C.RTLD_LOCAL) if tk.exists() else None
+        if self.testkit is not None:
+            for name, (res, args) in _TESTKIT_SIGS.items():
+                fn = getattr(self.testkit, name)
+                fn.restype = res
+                fn.argtypes = args
+                setattr(self, name, fn)
         g = self.nova_model_geometry()
         self.nh, self.nkv, self.hd, self.n_layers, self.kb = g.nh, g.nkv, g.hd, g.n_layers, g.kv_block
         self.group = self.nh // self.nkv

@@ -63,9 +63,6 @@ void     dev_graph_begin(nova_stream_t s);
 nova_graph_t dev_graph_end(nova_stream_t s);
 void     dev_graph_launch(nova_graph_t g, nova_stream_t s);
 void     dev_graph_destroy(nova_graph_t g);
-/* test kit (seeded synthetic data and a reference copy; not reference surfaces) */
-void     testkit_fill_normal_f16(uint16_t* p, uint64_t n, uint64_t seed, float scale, nova_stream_t s);
-void     testkit_copy(void* dst, const void* src, uint64_t bytes, nova_stream_t s);
 /* device facts */
 int      dev_cu_count(void);
 int      dev_count(void);                        /* 0 when no GPU is visible */

@@ -75,6 +75,13 @@ void launch_attn_prefill_paged(const float* q, const uint16_t* pool_k, const uin
  * Three launches on s: plan, split kernel, combine kernel.
  * n_keys[i] == 0 yields a zero output row. */
 size_t attn_decode_batch_workspace_bytes(int n_sess);
+/* Status word of the batched decode in `workspace` (n_sess as in the calls):
+ * 0, or an OR of failure bits set by the layers since the step's plan launch
+ * (1: a split workgroup's in-LDS partial exchange gave up waiting, and the
+ * heads it served were written as NaN).  The plan launch clears it.  Waits for
+ * the device to finish, then reads the word: a host-side check for tests and
+ * serving loops, not for the hot path. */
+int attn_decode_batch_status(const void* workspace, int n_sess);
 /* The batched call above = launch_attn_decode_plan + launch_attn_decode_paged_planned.
  * A decode step has the same n_keys and block tables in every layer, so a
  * caller can plan once per step and run only the planned call per layer:
@@ -127,20 +134,6 @@ void launch_attn_decode_paged_rope_batch(const float* q, const float* k_new, con
                                          const int32_t* tables, int table_stride, const int32_t* n_keys,
                                          int n_sess, int layer, int nb, float* o, void* workspace,
                                          nova_stream_t s);
-
-/* Test kit (not a reference surface): only the split kernel of
- * launch_attn_decode_paged_planned -- partials written, o not -- so that a
- * benchmark can time the dominant kernel alone on its own stream. */
-void testkit_attn_decode_split_only(const float* q, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
-                                    int table_stride, int n_sess, int layer, int nb, const uint16_t* k_new,
-                                    const uint16_t* v_new, void* workspace, nova_stream_t s);
-
-/* Test kit (not a reference surface): the HBM floor of the planned split --
- * the split grid of launch_attn_decode_paged_planned reading the same pages
- * with the same loads and no arithmetic (one sink word per thread into the
- * workspace's partial area).  Needs the step's launch_attn_decode_plan. */
-void testkit_decode_stream_floor(const uint16_t* pool_k, const uint16_t* pool_v, const int32_t* tables,
-                                 int table_stride, int n_sess, int layer, int nb, void* workspace, nova_stream_t s);
 
 /* Batched append: session i writes n tokens at positions pos0[i]..pos0[i]+n-1
  * (pos0: device int32[n_sess]) through tables + i*table_stride; k, v:

@@ -15,6 +15,7 @@
 #include <math.h>
 #include <pthread.h>
 #include <stdatomic.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -123,6 +124,16 @@ static void attend(cb_geom g, const float* qv, const int64_t* lim, int nq, const
     }
 }
 
+/* allocation or thread-start failures abort with a message (the reference's
+   abort-only convention): a lost unit would leave outputs uninitialised */
+static void* must(void* p, const char* what) {
+    if (!p) {
+        fprintf(stderr, "cpu_baseline: %s failed\n", what);
+        abort();
+    }
+    return p;
+}
+
 /* ---------------- thread pool over work units ---------------- */
 typedef struct {
     void (*fn)(void* ctx, int unit, float* scratch);
@@ -134,7 +145,8 @@ typedef struct {
 
 static void* pool_worker(void* p) {
     pool_job* j = (pool_job*)p;
-    float* scratch = (float*)aligned_alloc(64, (j->scratch_floats * sizeof(float) + 63) / 64 * 64);
+    float* scratch = (float*)must(aligned_alloc(64, (j->scratch_floats * sizeof(float) + 63) / 64 * 64 + 64),
+                                  "aligned_alloc");
     for (;;) {
         const int u = atomic_fetch_add(&j->next, 1);
         if (u >= j->n_units) break;
@@ -153,8 +165,9 @@ static void run_pool(void (*fn)(void*, int, float*), void* ctx, int n_units, siz
     j.scratch_floats = scratch_floats;
     if (n_threads < 1) n_threads = 1;
     if (n_threads > n_units) n_threads = n_units > 0 ? n_units : 1;
-    pthread_t* th = (pthread_t*)malloc(sizeof(pthread_t) * (size_t)n_threads);
-    for (int t = 0; t < n_threads; ++t) pthread_create(&th[t], NULL, pool_worker, &j);
+    pthread_t* th = (pthread_t*)must(malloc(sizeof(pthread_t) * (size_t)n_threads), "malloc");
+    for (int t = 0; t < n_threads; ++t)
+        if (pthread_create(&th[t], NULL, pool_worker, &j) != 0) must(NULL, "pthread_create");
     for (int t = 0; t < n_threads; ++t) pthread_join(th[t], NULL);
     free(th);
 }
@@ -218,8 +231,8 @@ void cb_attn_decode_batch(cb_geom g, const float* q, const uint16_t* pool_k, con
     const int hd = g.hd;
     if (g.kb > MAX_KB - 2 || hd > MAX_HD || hd % 16 || g.nh / g.nkv > 64) abort();
     int n_units = 0, n_slots = 0;
-    int* sess_split0 = (int*)malloc(sizeof(int) * (size_t)(n_sess + 1));
-    int* sess_nsplit = (int*)malloc(sizeof(int) * (size_t)(n_sess + 1));
+    int* sess_split0 = (int*)must(malloc(sizeof(int) * (size_t)(n_sess + 1)), "malloc");
+    int* sess_nsplit = (int*)must(malloc(sizeof(int) * (size_t)(n_sess + 1)), "malloc");
     for (int i = 0; i < n_sess; ++i) {
         const int pages = (int)((n_keys[i] + g.kb - 1) / g.kb);
         const int ns = (pages + SPLIT_PAGES - 1) / SPLIT_PAGES;
@@ -240,11 +253,11 @@ void cb_attn_decode_batch(cb_geom g, const float* q, const uint16_t* pool_k, con
     c.nb = nb;
     c.sess_split0 = sess_split0;
     c.sess_nsplit = sess_nsplit;
-    c.unit_sess = (int*)malloc(sizeof(int) * (size_t)(n_units + 1) * 4);
+    c.unit_sess = (int*)must(malloc(sizeof(int) * (size_t)(n_units + 1) * 4), "malloc");
     c.unit_kvh = c.unit_sess + (n_units + 1);
     c.unit_page = c.unit_kvh + (n_units + 1);
     c.unit_split = c.unit_page + (n_units + 1);
-    c.part = (float*)malloc(sizeof(float) * ((size_t)n_slots * g.nh * (hd + 2) + 1));
+    c.part = (float*)must(malloc(sizeof(float) * ((size_t)n_slots * g.nh * (hd + 2) + 1)), "malloc");
     int u = 0;
     for (int i = 0; i < n_sess; ++i)
         for (int sp = 0; sp < sess_nsplit[i]; ++sp)

@@ -9,11 +9,12 @@ import pytest
 
 ROOT = Path(__file__).resolve().parent.parent
 HEADERS = sorted((ROOT / "include").glob("*.h"))
+TESTKIT_HEADER = ROOT / "conflux-nova_amd" / "testkit" / "nova_testkit.h"
 
 
-def declared_functions():
+def declared_functions(headers=None):
     names = set()
-    for h in HEADERS:
+    for h in headers or HEADERS:
         text = re.sub(r"/\*.*?\*/", " ", h.read_text(), flags=re.S)
         text = re.sub(r"//[^\n]*", " ", text)
         for m in re.finditer(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\(", text):
@@ -46,12 +47,29 @@ def test_library_exports_every_declared_symbol(model):
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
     missing = sorted(declared_functions() - exported)
     assert not missing, missing
+    # and nothing else: the product library exports the contract and its
+    # marked extensions only (the test kit lives in its own library)
+    extra = sorted(exported - declared_functions())
+    assert not extra, extra
+    assert not any(n.startswith("testkit_") for n in exported)
+
+
+@pytest.mark.parametrize("model", ["qwen25_1p5b", "qwen25_7b", "qwen25_14b"])
+def test_testkit_library_exports_its_header(model):
+    import nova_amd
+    lib = nova_amd.testkit_path(model)
+    assert lib.exists(), f"{lib} not built"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib)], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert exported == declared_functions([TESTKIT_HEADER])
 
 
 def test_binding_covers_every_declared_symbol():
     import nova_amd
     missing = sorted(declared_functions() - set(nova_amd._SIGS))
     assert not missing, missing
+    assert set(nova_amd._TESTKIT_SIGS) == declared_functions([TESTKIT_HEADER])
+    assert not set(nova_amd._TESTKIT_SIGS) & set(nova_amd._SIGS)
 
 
 def test_library_loads_without_gpu(nova7):

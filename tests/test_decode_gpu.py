@@ -70,6 +70,7 @@ def _batch(nova, fx, q, tables, n_keys, k_new=None, v_new=None):
                                             do.ptr, ws.ptr, None)
         nova.dev_sync()
         outs.append(do.numpy(q.shape, np.float32))
+        assert nova.attn_decode_batch_status(ws.ptr, n) == 0   # no exchange gave up
     assert np.array_equal(outs[0], outs[1])
     return outs[0]
 
@@ -342,3 +343,64 @@ def test_stream_floor_reads_the_planned_pairs(nova7):
             assert (sink[w, 64 * wave:64 * wave + 64] == want).all(), (w, wave)
     for i in range(n):
         assert (covered[i] == 1).all(), i
+
+
+def test_decode_exchange_give_up_is_reported(nova7, oracle):
+    """The bounded LDS wait of the one-slot partial exchange (7B: two waves per
+    kv head) never gives up silently.  The test kit's copy of the planned call
+    sets the bound to 0 polls, so every exchange gives up (forced from the
+    host; every kernel still exits normally): the status word reads 1 and the
+    outputs are NaN.  The next plan clears the word, and the product call is
+    then correct with status 0."""
+    nova = nova7
+    assert nova.testkit is not None, "test kit library not built"
+    n_keys = np.array([300, 40, 1000], np.int32)
+    n = len(n_keys)
+    pages = (n_keys + 15) // 16
+    fx = PagedFixture(nova, nb=n * int(pages.max()) + 4, layer=LAYER, seed=91)
+    tables = fx.tables(n, int(pages.max()))
+    q = fx.rng.standard_normal((n, nova.nh, nova.hd)).astype(np.float32)
+    ws = nova.alloc(nova.attn_decode_batch_workspace_bytes(n))
+    dq, dt, dn = nova.upload(q), nova.upload(tables), nova.upload(n_keys)
+    do = nova.alloc(q.nbytes)
+    print("[case] decode exchange give-up forced (spin 0), 7B, 3 sessions", flush=True)
+    nova.launch_attn_decode_plan(dt.ptr, tables.shape[1], dn.ptr, n, ws.ptr, None)
+    nova.testkit_attn_decode_planned_spin(dq.ptr, fx.k.ptr, fx.v.ptr, dt.ptr, tables.shape[1], n, LAYER, fx.nb,
+                                          None, None, do.ptr, ws.ptr, 0, None)
+    nova.dev_sync()
+    assert nova.attn_decode_batch_status(ws.ptr, n) == 1
+    assert np.isnan(do.numpy(q.shape, np.float32)).all()
+    print("[case] decode after a give-up: plan clears the status", flush=True)
+    nova.launch_attn_decode_plan(dt.ptr, tables.shape[1], dn.ptr, n, ws.ptr, None)
+    assert nova.attn_decode_batch_status(ws.ptr, n) == 0
+    nova.testkit_attn_decode_planned_spin(dq.ptr, fx.k.ptr, fx.v.ptr, dt.ptr, tables.shape[1], n, LAYER, fx.nb,
+                                          None, None, do.ptr, ws.ptr, 1 << 22, None)
+    nova.dev_sync()
+    assert nova.attn_decode_batch_status(ws.ptr, n) == 0
+    got = do.numpy(q.shape, np.float32)
+    for i in range(n):
+        ref = oracle.attn_decode_paged("qwen25_7b", q[i], fx.hk, fx.hv, tables[i], 0, fx.nb, int(n_keys[i]))
+        assert_close(got[i], ref, what=f"session {i} after give-up")
+
+
+@pytest.mark.parametrize("n_keys", [[1000], [1009, 77], [4001, 33, 250]])
+def test_decode_batch_uneven_ranges_1p5b(n_keys, oracle):
+    """1.5B (four waves per kv head, a partial slot per wave row): the combine
+    reads only the rows that can hold a page pair, ceil(ceil(P/k)/2) per split
+    workgroup.  Page counts that k does not divide give ranges of unequal
+    length (e.g. 63 pages over 16 workgroups); every one of them must be
+    read."""
+    import nova_amd
+    nova = nova_amd.load("qwen25_1p5b")
+    n_keys = np.asarray(n_keys, np.int32)
+    n = len(n_keys)
+    max_pages = int((n_keys.max() + 15) // 16)
+    print(f"[case] decode batch uneven ranges 1.5B n_keys={n_keys.tolist()}", flush=True)
+    fx = PagedFixture(nova, nb=n * max_pages + 3, layer=LAYER, seed=int(n_keys.sum()))
+    tables = fx.tables(n, max_pages)
+    q = fx.rng.standard_normal((n, nova.nh, nova.hd)).astype(np.float32)
+    got = _batch(nova, fx, q, tables, n_keys)
+    for i in range(n):
+        ref = oracle.attn_decode_paged("qwen25_1p5b", np.ascontiguousarray(q[i]), fx.hk, fx.hv, tables[i], 0,
+                                       fx.nb, int(n_keys[i]))
+        assert_close(got[i], ref, what=f"session {i} n_keys={n_keys[i]}")

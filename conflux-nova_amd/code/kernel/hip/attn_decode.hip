@@ -89,7 +89,11 @@ constexpr int WAVES = NOVA_DECODE_WAVES;
 constexpr int THREADS = WAVES * 64;
 constexpr int R = WAVES / NKV;           // waves per kv head
 static_assert(WAVES % NKV == 0, "kv heads must divide the waves of a workgroup");
-constexpr int PW = HD + 2;               // partial row: m, l, acc[HD]
+constexpr int PW = HD + 2;               // partial row of the reference-signature scratch: m, l, acc[HD]
+#ifndef NOVA_DECODE_PWB
+#define NOVA_DECODE_PWB (HD + 4)
+#endif
+constexpr int PWB = NOVA_DECODE_PWB;     // batched workspace row: m, l, pad, pad, acc[HD] (16-byte aligned acc)
 constexpr int kMaxBatch = 1024;          // sessions per batched launch
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int64_t kPageBytes = (int64_t)kKvBlock * KVW * 2;
@@ -118,6 +122,8 @@ struct DecodeArgs {
     int wave_parts;          // 1: a partial slot per (workgroup, wave row), no in-workgroup merge
     int kv_split;            // 1: grid.y = kv head, all waves of a workgroup on that head (no fused append)
     int spin;                // polls of the in-workgroup exchange before it gives up (kSpinLimit)
+    int pw;                  // floats per partial row: {m, l, [pad,] acc[HD]}
+    int po;                  // offset of acc[0] in a row (2, or 4: 16-byte aligned acc)
     int32_t* status;         // batched path: the plan's status word (null: none)
 };
 
@@ -714,7 +720,7 @@ decode_split_kernel(DecodeArgs a) {
         // this wave's G rows of a partial slot, straight from the accumulators
         auto write_rows = [&](float* pout) {
             if (c < G) {
-                float* row = pout + (int64_t)(kvh * G + c) * PW;
+                float* row = pout + (int64_t)(kvh * G + c) * a.pw;
                 if (g == 0) {
                     row[0] = m;
                     row[1] = lsum;
@@ -727,7 +733,7 @@ decode_split_kernel(DecodeArgs a) {
                         lo4[cb] = acc[cb][ii];
                         hi4[cb] = acc[cb + 4][ii];
                     }
-                    float* dst = row + 2 + 8 * (4 * g + ii);
+                    float* dst = row + a.po + 8 * (4 * g + ii);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         dst[e] = lo4[e];
@@ -737,7 +743,7 @@ decode_split_kernel(DecodeArgs a) {
             }
         };
         if constexpr (R == 1 && !kKvSplit) {
-            write_rows(a.part + (int64_t)slot * NH * PW);
+            write_rows(a.part + (int64_t)slot * NH * a.pw);
         } else if (a.wave_parts == 2 && !kKvSplit) {
             // one partial slot per workgroup: the R waves of a kv head merge
             // through LDS with no serial pass.  Lane group g (head dims
@@ -818,7 +824,7 @@ decode_split_kernel(DecodeArgs a) {
                         }
                     }
                 }
-                float* row = a.part + ((int64_t)slot * NH + kvh * G + c) * PW;
+                float* row = a.part + ((int64_t)slot * NH + kvh * G + c) * a.pw;
                 if (gave_up) {
                     // the partner's rows may not be in LDS: poison this slot so
                     // that the combine's output for these heads is NaN
@@ -839,17 +845,17 @@ decode_split_kernel(DecodeArgs a) {
                         lo4[cb] = A[cb][ii];
                         hi4[cb] = A[cb + 4][ii];
                     }
-                    *reinterpret_cast<f4*>(row + 2 + 8 * (4 * g + ii)) = lo4;
-                    *reinterpret_cast<f4*>(row + 2 + 8 * (4 * g + ii) + 4) = hi4;
+                    *reinterpret_cast<f4*>(row + a.po + 8 * (4 * g + ii)) = lo4;
+                    *reinterpret_cast<f4*>(row + a.po + 8 * (4 * g + ii) + 4) = hi4;
                 }
             }
         } else if (a.wave_parts) {
             // slot w*R + r: the combine merges the R rows with the workgroups'
-            write_rows(a.part + ((int64_t)slot * R + r) * NH * PW);
+            write_rows(a.part + ((int64_t)slot * R + r) * NH * a.pw);
         } else {
             // merge the waves of each kv head in LDS (kv-split: the G heads of
             // this workgroup's kv head over all its waves)
-            float* pout = a.part + (int64_t)w * NH * PW;
+            float* pout = a.part + (int64_t)w * NH * a.pw;
             if (g == 0) {
                 s_m[wave][c] = m;
                 s_l[wave][c] = lsum;
@@ -887,10 +893,10 @@ decode_split_kernel(DecodeArgs a) {
                     L = fmaf(lw, f, L);
                     A = fmaf(s_acc[ww][hc][d], f, A);
                 }
-                pout[(int64_t)h * PW + 2 + d] = A;
+                pout[(int64_t)h * a.pw + a.po + d] = A;
                 if (d == 0) {
-                    pout[(int64_t)h * PW] = M;
-                    pout[(int64_t)h * PW + 1] = L;
+                    pout[(int64_t)h * a.pw] = M;
+                    pout[(int64_t)h * a.pw + 1] = L;
                 }
             }
         }
@@ -1027,7 +1033,7 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
         if (g == 0) *orow = f4{0.f, 0.f, 0.f, 0.f};
         return;
     }
-    constexpr int64_t SEG = (int64_t)NH * PW;
+    const int64_t SEG = (int64_t)NH * a.pw;
     constexpr int kChunk = 8;
     // partial slots per split workgroup; with one per wave row, only the rows
     // that can hold a page pair are read (a workgroup has at most
@@ -1036,7 +1042,7 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     const int stride = a.wave_parts == 1 ? R : 1;
     const int used = a.wave_parts == 1 ? min(R, (range_max_pages(pt.pages, pt.k) + 1) >> 1) : 1;
     const int n_rows = pt.k * used;
-    const float* base = a.part + (int64_t)pt.kc * stride * SEG + (int64_t)h * PW;
+    const float* base = a.part + (int64_t)pt.kc * stride * SEG + (int64_t)h * a.pw;
     float M = -INFINITY, L = 0.f;
     f4 A = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = g; s0 < n_rows; s0 += kCombGroups * kChunk) {
@@ -1051,7 +1057,7 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
             const float* row = base + (int64_t)(wg * stride + (sl - wg * used)) * SEG;
             ms[jj] = row[0];
             ls[jj] = in ? row[1] : 0.f;
-            as[jj] = *reinterpret_cast<const f4*>(row + 2 + 4 * q4);
+            as[jj] = *reinterpret_cast<const f4*>(row + a.po + 4 * q4);
         }
         float mc = M;
 #pragma unroll
@@ -1257,6 +1263,8 @@ DecodeArgs batch_args(const int32_t* tables, int table_stride, const int32_t* n_
     a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + plan_bytes(n_sess));
     a.spin = kSpinLimit;
     a.status = static_cast<int32_t*>(workspace) + plan_status_off(n_sess, a.gw);
+    a.pw = PWB;
+    a.po = PWB - HD;
     // Partial slots: with two waves per kv head (7B) they merge through LDS
     // into one slot per workgroup (half the partial bytes, same step time);
     // with four (1.5B) the exchange costs more than it saves: one slot per
@@ -1282,7 +1290,7 @@ constexpr int kStaticMaxSess = 64;
 constexpr int kStaticMaxCUs = 256;
 constexpr size_t kStaticPlanBytes = ((size_t)plan_ints(kStaticMaxSess, kStaticMaxCUs) * 4 + 255) / 256 * 256;
 constexpr size_t kStaticBytes =
-    kStaticPlanBytes + (size_t)split_slots(kStaticMaxSess, kStaticMaxCUs) * R * NH * PW * sizeof(float);
+    kStaticPlanBytes + (size_t)split_slots(kStaticMaxSess, kStaticMaxCUs) * R * NH * PWB * sizeof(float);
 __device__ __align__(256) unsigned char scratch[kStaticBytes];
 
 // Device address of `scratch` on the current device, looked up once per device
@@ -1320,7 +1328,7 @@ void nova_decode_trace_copy(void* host) { NOVA_HIP(hipMemcpyFromSymbol(host, HIP
 
 size_t attn_decode_batch_workspace_bytes(int n_sess) {
     NOVA_REQUIRE(n_sess >= 1 && n_sess <= kMaxBatch);
-    return plan_bytes(n_sess) + (size_t)split_slots(n_sess, batch_workgroups()) * R * NH * PW * sizeof(float);
+    return plan_bytes(n_sess) + (size_t)split_slots(n_sess, batch_workgroups()) * R * NH * PWB * sizeof(float);
 }
 
 void launch_attn_decode_plan(const int32_t* tables, int table_stride, const int32_t* n_keys, int n_sess,
@@ -1437,6 +1445,8 @@ void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint
     a.gw = gw;
     a.kv_split = 1;   // NKV workgroups per partial slot: 31 * NKV CUs per call
     a.spin = kSpinLimit;
+    a.pw = PW;        // the reference's scratch holds NH*32*(HD+2) floats
+    a.po = 2;
     launch_pair(a, 1, o, reinterpret_cast<hipStream_t>(s));
 }
 
@@ -1479,7 +1489,7 @@ void testkit_decode_stream_floor(const uint16_t* pool_k, const uint16_t* pool_v,
     a.pool_v = pool_v;
     a.layer = layer;
     a.nb = nb;
-    static_assert(THREADS <= R * NH * PW, "one sink word per thread fits in a workgroup's partial slots");
+    static_assert(THREADS <= R * NH * PWB, "one sink word per thread fits in a workgroup's partial slots");
     hipLaunchKernelGGL(decode_stream_floor_kernel, dim3(split_slots(n_sess, a.gw)), dim3(THREADS), 0,
                        reinterpret_cast<hipStream_t>(s), a);
     NOVA_LAUNCHED();

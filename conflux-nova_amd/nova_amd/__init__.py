@@ -17,7 +17,8 @@ from pathlib import Path
 import numpy as np
 
 PKG = Path(__file__).resolve().parent.parent
-LIB_DIR = PKG / "lib"
+# NOVA_LIB_DIR: an explicit alternative build directory (A/B measurements)
+LIB_DIR = Path(os.environ.get("NOVA_LIB_DIR", str(PKG / "lib")))
 MODELS = ("qwen25_1p5b", "qwen25_7b", "qwen25_14b")
 
 vp, i32, i64, u64, f32, sz = C.c_void_p, C.c_int, C.c_int64, C.c_uint64, C.c_float, C.c_size_t

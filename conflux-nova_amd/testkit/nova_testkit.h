@@ -27,7 +27,7 @@ void testkit_fill_normal_f16(uint16_t* p, uint64_t n, uint64_t seed, float scale
 void testkit_copy(void* dst, const void* src, uint64_t bytes, nova_stream_t s);
 
 /* Contiguous streaming read of `bytes` (a multiple of 16) by `workgroups`
- * workgroups of 512 threads, non-temporal 16-byte loads, one sink word per
+ * workgroups of 512 threads, non-temporal 16-byte loads with 16 per lane in flight, one sink word per
  * thread into `sink` (workgroups * 512 uint32): the HBM floor of reading a
  * layer's K/V bytes with no paging at all. */
 void testkit_stream_read(const void* src, uint64_t bytes, int workgroups, uint32_t* sink, nova_stream_t s);

@@ -317,11 +317,12 @@ def test_stream_floor_reads_the_planned_pairs(nova7):
     nova.launch_attn_decode_plan(dt.ptr, max_pages, dn.ptr, n, ws.ptr, None)
     nova.testkit_decode_stream_floor(k.ptr, v.ptr, dt.ptr, max_pages, n, 0, nb, ws.ptr, None)
     nova.dev_sync()
-    # workspace = plan (rounded to 256 B) + slots * R * NH * PW floats
-    R, PW, rec = 8 // nova.nkv, nova.hd + 2, 72
+    # workspace = plan (session table, combine map, slot records, status
+    # word; rounded to 256 B) + slots * R * NH * PW floats, PW = HD + 4
+    R, PW, rec = 8 // nova.nkv, nova.hd + 4, 72
     rec_off = n * 4 + n * nova.nh * 4
     slots = [s for s in range(1, 4096)
-             if -(-(rec_off + s * rec) * 4 // 256) * 256 + s * R * nova.nh * PW * 4 == ws_bytes]
+             if -(-(rec_off + s * rec + 1) * 4 // 256) * 256 + s * R * nova.nh * PW * 4 == ws_bytes]
     assert len(slots) == 1, slots
     slots = slots[0]
     plan_b = ws_bytes - slots * R * nova.nh * PW * 4

@@ -237,6 +237,31 @@ class DecodeWorkload:
             nv.dev_graph_destroy(g)
         return out["pair"], out["split"], out["floor"], out["contig"]
 
+    def solo_ms(self, steps, warmup):
+        """The same step through launch_attn_decode_paged_solo: one launch per
+        layer (one workgroup per (kv head, session) streams the session's
+        pages, merges on chip and writes O; fused append), no plan, no
+        partials, no combine; from a HIP graph, ms per step."""
+        nv, s, L = self.nova, self.s, self.layers
+        qs, kvs = self.n * nv.nh * nv.hd, self.n * nv.kvw
+        nv.dev_graph_begin(s)
+        for l in range(L):
+            nv.launch_attn_decode_paged_solo(
+                self.q.ptr + l * qs * 4, self.k.ptr, self.v.ptr, self.tables.ptr, self.max_pages, self.nk.ptr,
+                self.n, l, self.nb, self.knew.ptr + l * kvs * 2, self.vnew.ptr + l * kvs * 2,
+                self.o.ptr + l * qs * 4, s)
+        g = nv.dev_graph_end(s)
+        for _ in range(warmup):
+            nv.dev_graph_launch(g, s)
+        t = Timer(nv, s)
+        t.start()
+        for _ in range(steps):
+            nv.dev_graph_launch(g, s)
+        ms = t.stop() / steps
+        nv.dev_graph_destroy(g)
+        nv.dev_stream_sync(s)
+        return ms
+
     def per_session_ms(self, steps, warmup):
         """The reference's call pattern for the same step (Engine::decode_batch,
         src/model.cpp:282-289): per layer and session one launch_kv_store_paged
@@ -406,15 +431,27 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
                       "the split grid reading the same pages with the same loads, no arithmetic), the contiguous "
                       "floor (testkit_stream_read: the same bytes as one contiguous read, one workgroup per CU); "
                       "step_frac = the timed step incl. the plan kernel"}
+    # the one-launch solo path (one CU per session and kv head): timed where
+    # its sessions are short enough to finish in minutes at this step count
+    got_split = nova.download(wl.o, (wl.n, nova.nh, nova.hd), np.float32)
+    solo_ms = None
+    if wl.max_pages <= 128:
+        print("[leg] solo step", file=sys.stderr, flush=True)
+        solo_ms = wl.solo_ms(args.steps, args.warmup)
+    got_solo = nova.download(wl.o, (wl.n, nova.nh, nova.hd), np.float32) if solo_ms else None
     cpu = None
     parity = None
     if not args.no_cpu:
         th = cpu_threads(args)
         secs, out = wl.cpu_sample(0, th)
-        # parity at full size on layer 0 (GPU output of the last replay)
-        got = nova.download(wl.o, (wl.n, nova.nh, nova.hd), np.float32)
-        err = float(np.abs(got - out).max())
+        # parity at full size on layer 0 (GPU output of the last replay of each path)
+        err = float(np.abs(got_split - out).max())
         parity = {"layer0_max_abs_err": err, "ok": err <= 2e-3}
+        if got_solo is not None:
+            err_solo = float(np.abs(got_solo - out).max())
+            parity["solo_layer0_max_abs_err"] = err_solo
+            parity["ok"] = parity["ok"] and err_solo <= 2e-3
+            err = max(err, err_solo)
         if not parity["ok"]:
             print(f"bench: PARITY FAILURE on layer 0: max|gpu-cpu| = {err:.3e}", file=sys.stderr, flush=True)
         cpu_gbs = (bytes_step / wl.layers) / secs / 1e9
@@ -439,6 +476,29 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
         "data": "synthetic (seeded N(0,1) K/V, Q; seeded ragged contexts and page shuffle)",
         "config": metric_cfg["config"], "roofline": roof, "cpu_baseline": cpu,
     }
+    if solo_ms is not None:
+        solo = {"ms_per_step": round(solo_ms, 4), "GBs": round(bytes_step / (solo_ms * 1e-3) / 1e9, 1),
+                "pct_hbm_peak": round(100 * bytes_step / (solo_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 2),
+                "us_per_layer": round(solo_ms * 1e3 / wl.layers, 2),
+                "what": "the same step through launch_attn_decode_paged_solo: one launch per layer, one "
+                        "workgroup per (kv head, session) streaming the session's pages, output written by the "
+                        "split kernel (no plan, no partials, no combine launch), fused append"}
+        if solo_ms < ms:
+            # the faster path leads the line; the planned split path stays beside it
+            split = {"ms_per_step": line["ms_per_step"], "GBs": line["value"], "pct_hbm_peak": line["pct_hbm_peak"],
+                     "what": "plan + 28 x launch_attn_decode_paged_planned (split + combine), from a HIP graph",
+                     "roofline": roof}
+            sgbs = bytes_step / (solo_ms * 1e-3) / 1e9
+            line.update({"value": round(sgbs, 2), "ms_per_step": round(solo_ms, 4),
+                         "us_per_step": round(solo_ms * 1e3, 2), "pct_hbm_peak": round(100 * sgbs / HBM_PEAK_GBS, 2),
+                         "path": "solo (launch_attn_decode_paged_solo)", "split_path": split})
+            line["roofline"] = {"bound": "hbm", "achieved": round(sgbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                "frac": round(sgbs / HBM_PEAK_GBS, 4), "traffic": load_traffic(workload_name + "_solo"),
+                                "kernel": "decode_split_kernel<solo> (one launch per layer: the whole step's work)",
+                                "kernel_us": round(solo_ms * 1e3 / wl.layers, 2), "bytes_per_launch": bytes_launch,
+                                "timing": "HIP events around graph replays of the step's 28 solo launches"}
+        else:
+            line["solo_path"] = solo
     if parity:
         line["parity"] = parity
     if per_session:

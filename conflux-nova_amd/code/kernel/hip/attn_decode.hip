@@ -120,7 +120,9 @@ struct DecodeArgs {
     const int32_t* plan;     // per-step plan (null: derive the partition in-kernel)
     int gw;                  // workgroups in the grid
     int wave_parts;          // 1: a partial slot per (workgroup, wave row), no in-workgroup merge
-    int kv_split;            // 1: grid.y = kv head, all waves of a workgroup on that head (no fused append)
+    int kv_split;            // 1: grid.x = kv head, all waves of a workgroup on that head
+    float* o;                // solo launches: the output [n_sess][NH][HD], written by the split kernel
+    int tab_read;            // solo launches: block-table entries of a row that may be read before n_keys is known
     int spin;                // polls of the in-workgroup exchange before it gives up (kSpinLimit)
     int pw;                  // floats per partial row: {m, l, [pad,] acc[HD]}
     int po;                  // offset of acc[0] in a row (2, or 4: 16-byte aligned acc)
@@ -359,9 +361,15 @@ __device__ __forceinline__ u4 k_operand(const u4* kl, int ks) {
     return r;
 }
 
-template <bool kRope, bool kKvSplit>
+// kSolo (with kKvSplit): one workgroup per (kv head, session) streams all of
+// the session's pages for that head, merges its waves in LDS and writes the
+// output rows itself -- no partial rows, no combine launch.  For steps whose
+// sessions are short enough that one CU streams a session's head in about
+// the time a second launch would cost.
+template <bool kRope, bool kKvSplit, bool kSolo = false>
 __global__ void __launch_bounds__(THREADS)
 decode_split_kernel(DecodeArgs a) {
+    static_assert(!kSolo || kKvSplit, "solo workgroups serve one kv head");
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];
     __shared__ float s_acc[(R > 1 || kKvSplit) ? WAVES : 1][G][HD];
@@ -370,7 +378,8 @@ decode_split_kernel(DecodeArgs a) {
     __shared__ int s_ready[WAVES];               // a wave's exchange rows are in LDS (one-slot partials)
 
     const int tid = threadIdx.x;
-    const int wave = tid >> 6;
+    // solo: the wave index (and the pair loop) kept in scalar registers
+    const int wave = kSolo ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int lane = tid & 63;
     const int g = lane >> 4;      // 0..3
     const int c = lane & 15;      // 0..15
@@ -386,7 +395,23 @@ decode_split_kernel(DecodeArgs a) {
     if (wave == 0) TRACE(0);
 
     int i, n_keys, pa, pb, tv, slot = w;        // slot: this workgroup's partial row index
-    if (a.plan) {
+    int tv2 = 0;                                 // solo: table entries 64..127
+    if constexpr (kSolo) {
+        // session w, all its pages; the first table entries load beside n_keys
+        // (tab_read entries of every row are readable), not after it
+        i = w;
+        const int32_t* trow = a.tables + (int64_t)i * a.table_stride;
+        tv = lane < a.tab_read ? trow[lane] : 0;
+        tv2 = 64 + lane < a.tab_read ? trow[64 + lane] : 0;
+        n_keys = nkeys_of(a, i);
+        pa = 0;
+        pb = n_keys > 0 ? (n_keys + kKvBlock - 1) >> kKvBlockShift : 0;
+        if (n_keys <= 0) {                       // no keys: zero rows (uniform)
+            float* orow = a.o + ((int64_t)i * NH + kvh * G) * HD;
+            for (int e = tid; e < G * HD / 4; e += THREADS) reinterpret_cast<f4*>(orow)[e] = f4{0.f, 0.f, 0.f, 0.f};
+            return;
+        }
+    } else if (a.plan) {
         // one load: lane t holds phys[t]; lanes 0..3 the header
         const int32_t* rec = a.plan + plan_rec_off(a.n_sess) + (int64_t)w * kRec;
         tv = rec[lane];
@@ -411,6 +436,7 @@ decode_split_kernel(DecodeArgs a) {
     // otherwise the compiler's wait before its first read, after the query and
     // first-pair loads below are issued, would be a wait for all of them
     asm volatile("v_mov_b32 %0, %1" : "=v"(tv) : "v"(tv));
+    if constexpr (kSolo) asm volatile("v_mov_b32 %0, %1" : "=v"(tv2) : "v"(tv2));
     const int last_page = (n_keys - 1) >> kKvBlockShift;
     const int32_t* table = a.tables + (int64_t)i * a.table_stride;
 
@@ -429,6 +455,15 @@ decode_split_kernel(DecodeArgs a) {
         int tchunk = 0;
         auto phys_of = [&](int pg) -> int {
             const int rel = pg - pa;
+            if constexpr (kSolo) {
+                // the first 128 entries sit in tv, tv2; later pages come one at
+                // a time through the scalar cache.  No vector load in the pair
+                // loop but the pairs', so the compiler's waits count exactly and
+                // the prefetched pair stays in flight during the arithmetic.
+                if (rel < 64) return __builtin_amdgcn_readlane(tv, rel);
+                if (rel < 128) return __builtin_amdgcn_readlane(tv2, rel - 64);
+                return *(const __attribute__((address_space(4))) int32_t*)(uintptr_t)(table + pg);
+            }
             if ((rel >> 6) != tchunk) {          // rare: ranges longer than 64 pages
                 tchunk = rel >> 6;
                 const int e = pa + 64 * tchunk + lane;
@@ -441,28 +476,33 @@ decode_split_kernel(DecodeArgs a) {
         // kFirst: a wave's first pair (pages < 16 into the range) takes its pages
         // straight from the slice register, with no reload branch: a reload's
         // load would make the first pair's issue wait for every load before it
-        auto load_pair = [&](auto first_tag, int qp, PairRegs& pr) {
+        // live == false: the same 16 loads, all lanes on the layer's first
+        // 16 bytes (one cached line), for a prefetch slot with no pair left --
+        // a load under a branch would make the compiler drain every load in
+        // flight before the next use of any of them
+        auto load_pair = [&](auto first_tag, int qp, PairRegs& pr, bool live = true) {
             constexpr bool kFirst = decltype(first_tag)::value;
             const int pg0 = pa + 2 * qp;
             const int pg1 = pg0 + 1 < pb ? pg0 + 1 : pg0;   // a lone last page loads itself twice
             const int ph0 = kFirst ? __builtin_amdgcn_readlane(tv, pg0 - pa) : phys_of(pg0);
             const int ph1 = kFirst ? __builtin_amdgcn_readlane(tv, pg1 - pa) : phys_of(pg1);
-            const int64_t b0 = (layer_page0 + ph0) * kPageBytes;
-            const int64_t b1 = (layer_page0 + ph1) * kPageBytes;
+            const int64_t b0 = (layer_page0 + (live ? ph0 : 0)) * kPageBytes;
+            const int64_t b1 = (layer_page0 + (live ? ph1 : 0)) * kPageBytes;
+            const uint32_t lm = live ? ~0u : 0u;
             const char* k0 = pk + b0;
             const char* k1 = pk + b1;
             const char* v0 = pv + b0;
             const char* v1 = pv + b1;
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const uint32_t o = koff + (ks & 1) * 8 * kRowBytes + (ks >> 1) * 128;
+                const uint32_t o = (koff + (ks & 1) * 8 * kRowBytes + (ks >> 1) * 128) & lm;
                 pr.k0[ks] = ld16_nt(k0, o);
                 pr.k1[ks] = ld16_nt(k1, o);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                pr.v[j] = ld16_nt(v0, voff[j]);
-                pr.v[4 + j] = ld16_nt(v1, voff[j]);
+                pr.v[j] = ld16_nt(v0, voff[j] & lm);
+                pr.v[4 + j] = ld16_nt(v1, voff[j] & lm);
             }
         };
 
@@ -479,12 +519,15 @@ decode_split_kernel(DecodeArgs a) {
         // use for one reads a valid line and drops it.
         const int phys_last = table[last_page];     // the appended token's page (may lie past the slice register)
         static_assert(KVW / 8 <= THREADS, "one 16-byte piece of the appended row per thread");
-        const bool app_thread = !kRope && appends && tid < KVW / 8;
+        // (a kv-split workgroup appends its own kv head's part of the row)
+        constexpr int kAppW = kKvSplit ? HD : KVW;      // halfs of the row this workgroup appends
+        const int app_off = kKvSplit ? kvh * HD : 0;
+        const bool app_thread = !kRope && appends && tid < kAppW / 8;
         u4 knew, vnew;
         {
             const uint16_t* ks = a.k_new ? a.k_new : reinterpret_cast<const uint16_t*>(a.q);
             const uint16_t* vs = a.v_new ? a.v_new : reinterpret_cast<const uint16_t*>(a.q);
-            const int64_t src = app_thread ? (int64_t)i * KVW + 8 * tid : 0;
+            const int64_t src = app_thread ? (int64_t)i * KVW + app_off + 8 * tid : 0;
             knew = *reinterpret_cast<const u4*>(ks + src);
             vnew = *reinterpret_cast<const u4*>(vs + src);
         }
@@ -507,8 +550,8 @@ decode_split_kernel(DecodeArgs a) {
         float rk0 = 0.f, rk1 = 0.f, rc = 0.f, rs = 0.f;
         float2 rv = {0.f, 0.f};
         static_assert(!kRope || (NKV * (HD / 2) <= THREADS && KVW <= 2 * THREADS), "one k pair and two v values per thread");
-        const bool rope_k = kRope && appends && tid < NKV * (HD / 2);
-        const bool rope_v = kRope && appends && 2 * tid < KVW;
+        const bool rope_k = kRope && appends && tid < (kAppW / HD) * (HD / 2);
+        const bool rope_v = kRope && appends && 2 * tid < kAppW;
         if constexpr (kRope) {
             const int64_t row = (int64_t)(n_keys - 1) * (HD / 2);
 #pragma unroll
@@ -518,13 +561,13 @@ decode_split_kernel(DecodeArgs a) {
                 rsn[2 * ks] = *reinterpret_cast<const f4*>(a.sn + row + 32 * ks + 8 * g);
                 rsn[2 * ks + 1] = *reinterpret_cast<const f4*>(a.sn + row + 32 * ks + 8 * g + 4);
             }
-            const int h = tid / (HD / 2), d = tid - h * (HD / 2);
+            const int h = kKvSplit ? kvh : tid / (HD / 2), d = kKvSplit ? tid : tid - h * (HD / 2);
             const int64_t kr = rope_k ? (int64_t)i * KVW + h * HD + d : 0;
             rk0 = a.k_new32[kr];
             rk1 = a.k_new32[kr + HD / 2];
             rc = a.cs[row + (rope_k ? d : 0)];
             rs = a.sn[row + (rope_k ? d : 0)];
-            rv = *reinterpret_cast<const float2*>(a.v_new32 + (rope_v ? (int64_t)i * KVW + 2 * tid : 0));
+            rv = *reinterpret_cast<const float2*>(a.v_new32 + (rope_v ? (int64_t)i * KVW + app_off + 2 * tid : 0));
         }
         asm volatile("" ::: "memory");   // keep the loads above ahead of the pair's in issue order
         PairRegs cur;
@@ -546,20 +589,20 @@ decode_split_kernel(DecodeArgs a) {
                 uint16_t* pv16 = const_cast<uint16_t*>(a.pool_v) + dst;
                 (void)src;
                 if (rope_k) {
-                    const int h = tid / (HD / 2), d = tid - h * (HD / 2);
+                    const int h = kKvSplit ? kvh : tid / (HD / 2), d = kKvSplit ? tid : tid - h * (HD / 2);
                     float y0, y1;
                     rope_rotate(rk0, rk1, rc, rs, y0, y1);
                     pk16[h * HD + d] = __builtin_bit_cast(uint16_t, (_Float16)y0);
                     pk16[h * HD + d + HD / 2] = __builtin_bit_cast(uint16_t, (_Float16)y1);
                 }
                 if (rope_v) {
-                    pv16[2 * tid] = __builtin_bit_cast(uint16_t, (_Float16)rv.x);
-                    pv16[2 * tid + 1] = __builtin_bit_cast(uint16_t, (_Float16)rv.y);
+                    pv16[app_off + 2 * tid] = __builtin_bit_cast(uint16_t, (_Float16)rv.x);
+                    pv16[app_off + 2 * tid + 1] = __builtin_bit_cast(uint16_t, (_Float16)rv.y);
                 }
             } else if (app_thread) {
                 (void)src;
-                *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_k) + dst + 8 * tid) = knew;
-                *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_v) + dst + 8 * tid) = vnew;
+                *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_k) + dst + app_off + 8 * tid) = knew;
+                *reinterpret_cast<u4*>(const_cast<uint16_t*>(a.pool_v) + dst + app_off + 8 * tid) = vnew;
             }
         }
 
@@ -708,10 +751,29 @@ decode_split_kernel(DecodeArgs a) {
         // overlap each other's latency (measured: a second pair prefetched
         // before the query conversion only delays the query rows further
         // behind the chip's first burst, 0.778 -> 0.791 ms per config-2 step)
-        for (int qp = r; qp < npairs; qp += RS) {
-            if (qp != r || !early) load_pair(std::false_type{}, qp, cur);
-            compute_pair(qp, cur);
-            if (wave == 0 && qp == r) TRACE(2);
+        if constexpr (kSolo) {
+            // one CU streams the whole session's head: the next pair's loads
+            // go out before this pair's arithmetic (two pairs in flight per
+            // wave), so the CU's stream does not stop at every pair
+            // Two register sets take turns (no copy between them: a copy would
+            // wait for the prefetch to land).
+            if (!early && r < npairs) load_pair(std::false_type{}, r, cur);
+            PairRegs alt;
+            for (int qp = r; qp < npairs; qp += 2 * RS) {
+                const bool m1 = qp + RS < npairs;
+                load_pair(std::false_type{}, m1 ? qp + RS : qp, alt, m1);
+                compute_pair(qp, cur);
+                if (!m1) break;
+                const bool m2 = qp + 2 * RS < npairs;
+                load_pair(std::false_type{}, m2 ? qp + 2 * RS : qp, cur, m2);
+                compute_pair(qp + RS, alt);
+            }
+        } else {
+            for (int qp = r; qp < npairs; qp += RS) {
+                if (qp != r || !early) load_pair(std::false_type{}, qp, cur);
+                compute_pair(qp, cur);
+                if (wave == 0 && qp == r) TRACE(2);
+            }
         }
         if (wave == 0) TRACE(3);
 
@@ -855,7 +917,7 @@ decode_split_kernel(DecodeArgs a) {
         } else {
             // merge the waves of each kv head in LDS (kv-split: the G heads of
             // this workgroup's kv head over all its waves)
-            float* pout = a.part + (int64_t)w * NH * a.pw;
+            float* pout = kSolo ? nullptr : a.part + (int64_t)w * NH * a.pw;
             if (g == 0) {
                 s_m[wave][c] = m;
                 s_l[wave][c] = lsum;
@@ -893,10 +955,14 @@ decode_split_kernel(DecodeArgs a) {
                     L = fmaf(lw, f, L);
                     A = fmaf(s_acc[ww][hc][d], f, A);
                 }
-                pout[(int64_t)h * a.pw + a.po + d] = A;
-                if (d == 0) {
-                    pout[(int64_t)h * a.pw] = M;
-                    pout[(int64_t)h * a.pw + 1] = L;
+                if constexpr (kSolo) {
+                    a.o[((int64_t)i * NH + h) * HD + d] = L > 0.f ? A / L : 0.f;
+                } else {
+                    pout[(int64_t)h * a.pw + a.po + d] = A;
+                    if (d == 0) {
+                        pout[(int64_t)h * a.pw] = M;
+                        pout[(int64_t)h * a.pw + 1] = L;
+                    }
                 }
             }
         }
@@ -1240,6 +1306,25 @@ void launch_split(const DecodeArgs& a, int n_sess, hipStream_t st) {
     NOVA_LAUNCHED();
 }
 
+// Solo launch: grid (kv head, session), the output written by the split
+// kernel.  Up to this many pages the reference-signature decode runs as one
+// solo launch instead of the split + combine pair.  Measured per layer (the
+// reference's launch_kv_store_paged + launch_attn_decode_paged, graph of 28
+// layers): 64 tokens 7.9 vs 14.4 us, 512 tokens 12.3 vs 14.2 us, 768 tokens
+// 14.8 vs 14.3 us (1.5B; 7B alike).  One CU's arithmetic, ~2.3 us per round
+// of one page pair per wave, is what limits a solo workgroup.
+#ifndef NOVA_DECODE_SOLO_PAGES
+#define NOVA_DECODE_SOLO_PAGES 40
+#endif
+constexpr int kSoloMaxPages = NOVA_DECODE_SOLO_PAGES;
+void launch_solo(const DecodeArgs& a, int n_sess, hipStream_t st) {
+    NOVA_REQUIRE(a.o && a.tab_read >= 1 && a.tab_read <= 128 && n_sess >= 1 && n_sess <= 65535);
+    const dim3 grid(NKV, n_sess);
+    if (a.cs) hipLaunchKernelGGL((decode_split_kernel<true, true, true>), grid, dim3(THREADS), 0, st, a);
+    else hipLaunchKernelGGL((decode_split_kernel<false, true, true>), grid, dim3(THREADS), 0, st, a);
+    NOVA_LAUNCHED();
+}
+
 void launch_pair(const DecodeArgs& a, int n_sess, float* o, hipStream_t st) {
     launch_split(a, n_sess, st);
     const int comb = a.plan ? n_sess * NH : a.kv_split ? 8 * ((NH + 7) / 8) : n_sess * NH;
@@ -1425,6 +1510,26 @@ void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint
     NOVA_REQUIRE(q && pool_k && pool_v && table && o && scratch);
     NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0 && n_keys >= 1);
     const int pages = (n_keys + kKvBlock - 1) >> kKvBlockShift;
+    if (pages <= kSoloMaxPages) {
+        // short context: NKV workgroups stream the whole table and write o
+        // directly (one launch; scratch is not touched)
+        DecodeArgs a{};
+        a.q = q;
+        a.pool_k = pool_k;
+        a.pool_v = pool_v;
+        a.tables = table;
+        a.table_stride = pages;
+        a.n_keys_scalar = n_keys;
+        a.n_sess = 1;
+        a.layer = layer;
+        a.nb = nb;
+        a.kv_split = 1;
+        a.o = o;
+        a.tab_read = pages < 128 ? pages : 128;
+        a.spin = kSpinLimit;
+        launch_solo(a, 1, reinterpret_cast<hipStream_t>(s));
+        return;
+    }
     // scratch holds NH*32*(HD+2) floats (reference contract): at most 32
     // partial slots, and the partition uses at most gw + 1 of them
     int gw = (pages + 1) / 2;
@@ -1448,6 +1553,60 @@ void launch_attn_decode_paged(const float* q, const uint16_t* pool_k, const uint
     a.pw = PW;        // the reference's scratch holds NH*32*(HD+2) floats
     a.po = 2;
     launch_pair(a, 1, o, reinterpret_cast<hipStream_t>(s));
+}
+
+void launch_attn_decode_paged_solo(const float* q, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
+                                   int table_stride, const int32_t* n_keys, int n_sess, int layer, int nb,
+                                   const uint16_t* k_new, const uint16_t* v_new, float* o, nova_stream_t s) {
+    NOVA_REQUIRE(q && pool_k && pool_v && tables && n_keys && o);
+    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0 && table_stride > 0);
+    NOVA_REQUIRE(n_sess >= 1 && n_sess <= 65535);
+    NOVA_REQUIRE((k_new == nullptr) == (v_new == nullptr));
+    DecodeArgs a{};
+    a.q = q;
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.tables = tables;
+    a.table_stride = table_stride;
+    a.n_keys = n_keys;
+    a.n_sess = n_sess;
+    a.layer = layer;
+    a.nb = nb;
+    a.k_new = k_new;
+    a.v_new = v_new;
+    a.kv_split = 1;
+    a.o = o;
+    a.tab_read = table_stride < 128 ? table_stride : 128;
+    a.spin = kSpinLimit;
+    launch_solo(a, n_sess, reinterpret_cast<hipStream_t>(s));
+}
+
+void launch_attn_decode_paged_rope_solo(const float* q, const float* k_new, const float* v_new, const float* cs,
+                                        const float* sn, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
+                                        int table_stride, const int32_t* n_keys, int n_sess, int layer, int nb,
+                                        float* o, nova_stream_t s) {
+    NOVA_REQUIRE(q && k_new && v_new && cs && sn && pool_k && pool_v && tables && n_keys && o);
+    NOVA_REQUIRE(layer >= 0 && layer < Model::L && nb > 0 && table_stride > 0);
+    NOVA_REQUIRE(n_sess >= 1 && n_sess <= 65535);
+    DecodeArgs a{};
+    a.q = q;
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.tables = tables;
+    a.table_stride = table_stride;
+    a.n_keys = n_keys;
+    a.n_sess = n_sess;
+    a.layer = layer;
+    a.nb = nb;
+    a.k_new32 = k_new;
+    a.v_new32 = v_new;
+    a.cs = cs;
+    a.sn = sn;
+    a.kv_split = 1;
+    a.o = o;
+    a.tab_read = table_stride < 128 ? table_stride : 128;
+    a.spin = kSpinLimit;
+    launch_solo(a, n_sess, reinterpret_cast<hipStream_t>(s));
 }
 
 int attn_decode_batch_status(const void* workspace, int n_sess) {

@@ -74,6 +74,8 @@ _SIGS = {
     "launch_attn_decode_paged_rope_batch": (None, [vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp]),
     "launch_attn_decode_paged_batch": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp, vp, vp]),
     "launch_attn_decode_paged_batch_noalloc": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp, vp]),
+    "launch_attn_decode_paged_solo": (None, [vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp, vp, vp]),
+    "launch_attn_decode_paged_rope_solo": (None, [vp, vp, vp, vp, vp, vp, vp, vp, i32, vp, i32, i32, i32, vp, vp]),
     "attn_decode_batch_status": (i32, [vp, i32]),
     "launch_attn_decode_plan": (None, [vp, i32, vp, i32, vp, vp]),
     "launch_attn_decode_paged_planned": (None, [vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, vp, vp, vp]),

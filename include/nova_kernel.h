@@ -135,6 +135,27 @@ void launch_attn_decode_paged_rope_batch(const float* q, const float* k_new, con
                                          int n_sess, int layer, int nb, float* o, void* workspace,
                                          nova_stream_t s);
 
+/* Batched decode in ONE launch for short contexts ("solo"): one workgroup
+ * per (kv head, session) streams all of the session's pages for that head,
+ * merges its waves on chip and writes the session's output rows itself: no
+ * plan, no partials, no combine launch, no workspace.  Arguments as for
+ * launch_attn_decode_paged_batch (k_new, v_new: NULL or the fused 1-token
+ * append), except that `tables` must hold n_sess full rows of table_stride
+ * readable entries (the first min(128, table_stride) entries of a row are read
+ * before its n_keys is known).  One CU serves a session's kv head, so this
+ * suits steps whose sessions hold up to about 40 pages (640 tokens); longer
+ * sessions belong on the split path (on config 1's single 1025-key session
+ * the split path is faster).  The reference's launch_attn_decode_paged takes
+ * this route itself for contexts up to 40 pages.  The _rope_ form fuses RoPE
+ * as launch_attn_decode_paged_rope_planned does. */
+void launch_attn_decode_paged_solo(const float* q, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
+                                   int table_stride, const int32_t* n_keys, int n_sess, int layer, int nb,
+                                   const uint16_t* k_new, const uint16_t* v_new, float* o, nova_stream_t s);
+void launch_attn_decode_paged_rope_solo(const float* q, const float* k_new, const float* v_new, const float* cs,
+                                        const float* sn, uint16_t* pool_k, uint16_t* pool_v, const int32_t* tables,
+                                        int table_stride, const int32_t* n_keys, int n_sess, int layer, int nb,
+                                        float* o, nova_stream_t s);
+
 /* Batched append: session i writes n tokens at positions pos0[i]..pos0[i]+n-1
  * (pos0: device int32[n_sess]) through tables + i*table_stride; k, v:
  * [n_sess][n][NKV][HD] fp16.  One launch for a decode step's appends (or a

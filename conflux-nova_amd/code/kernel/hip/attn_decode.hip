@@ -51,8 +51,10 @@
 //    product is two MFMAs accumulating in fp32, leaving ~2^-22 relative error
 //    per operand instead of fp16's 2^-11.  The matrix cores have the slack:
 //    the kernel is bound by HBM, not by MFMA issue.
-//  * Online softmax in the log2 domain (exp2f), scale*log2(e) folded into the
-//    per-head factor.  Split partials merge with the reference's combine rule
+//  * Online softmax in the log2 domain (raw v_exp_f32), scale*log2(e) folded
+//    into the per-head factor, with a lazy running max: it moves only when a
+//    score exceeds it by more than 8, so most pairs skip the cross-lane max
+//    and the accumulator rescale.  Split partials merge with the reference's combine rule
 //    (max, then l- and acc-weighted sums; rows with l == 0 are skipped) in a
 //    second, small kernel: the kernel boundary publishes the partials, so no
 //    workgroup pays for a device-scope fence (an L2 writeback on this part).
@@ -96,6 +98,7 @@ constexpr int PW = HD + 2;               // partial row of the reference-signatu
 constexpr int PWB = NOVA_DECODE_PWB;     // batched workspace row: m, l, pad, pad, acc[HD] (16-byte aligned acc)
 constexpr int kMaxBatch = 1024;          // sessions per batched launch
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazy = 8.0f;            // running-max slack, log2 units (weights <= 2^8)
 constexpr int64_t kPageBytes = (int64_t)kKvBlock * KVW * 2;
 constexpr int kRowBytes = KVW * 2;
 
@@ -366,10 +369,14 @@ __device__ __forceinline__ u4 k_operand(const u4* kl, int ks) {
 // output rows itself -- no partial rows, no combine launch.  For steps whose
 // sessions are short enough that one CU streams a session's head in about
 // the time a second launch would cost.
-template <bool kRope, bool kKvSplit, bool kSolo = false>
+// kSingle (planned launches of one session): the session is known before the
+// plan record arrives, so the query rows and the new token's row are loaded
+// beside the record instead of one round trip after it.
+template <bool kRope, bool kKvSplit, bool kSolo = false, bool kSingle = false>
 __global__ void __launch_bounds__(THREADS)
 decode_split_kernel(DecodeArgs a) {
     static_assert(!kSolo || kKvSplit, "solo workgroups serve one kv head");
+    static_assert(!kSingle || !kKvSplit, "single-session launches use the planned grid");
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];
     __shared__ float s_acc[(R > 1 || kKvSplit) ? WAVES : 1][G][HD];
@@ -396,6 +403,36 @@ decode_split_kernel(DecodeArgs a) {
 
     int i, n_keys, pa, pb, tv, slot = w;        // slot: this workgroup's partial row index
     int tv2 = 0;                                 // solo: table entries 64..127
+
+    // The appended token's row piece of this thread and the query rows of
+    // session `sess`.  Every wave issues the same loads in the same order,
+    // whatever its role, so that the compiler's waits count exactly: a wave
+    // without a use for one reads a valid line and drops it.
+    // (a kv-split workgroup appends its own kv head's part of the row)
+    constexpr int kAppW = kKvSplit ? HD : KVW;      // halfs of the row this workgroup appends
+    const int app_off = kKvSplit ? kvh * HD : 0;
+    const bool app_lane = !kRope && tid < kAppW / 8;
+    const bool qreal = c < G;
+    u4 knew, vnew;
+    f4 qraw[8];
+    auto issue_new = [&](int sess) {
+        const uint16_t* ks = a.k_new ? a.k_new : reinterpret_cast<const uint16_t*>(a.q);
+        const uint16_t* vs = a.v_new ? a.v_new : reinterpret_cast<const uint16_t*>(a.q);
+        const int64_t src = app_lane ? (int64_t)sess * KVW + app_off + 8 * tid : 0;
+        knew = *reinterpret_cast<const u4*>(ks + src);
+        vnew = *reinterpret_cast<const u4*>(vs + src);
+    };
+    auto issue_q = [&](int sess) {
+        // the converting wave of each kv head (r == 0) reads its rows; the others one line
+        const int64_t qoff = r == 0 ? ((int64_t)sess * NH + kvh * G + (qreal ? c : 0)) * HD + 8 * g : (int64_t)sess * NH * HD;
+        const int step = r == 0 ? 1 : 0;
+        const float* qp = a.q + qoff;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            qraw[2 * ks] = *reinterpret_cast<const f4*>(qp + step * (32 * ks));
+            qraw[2 * ks + 1] = *reinterpret_cast<const f4*>(qp + step * (32 * ks + 4));
+        }
+    };
     if constexpr (kSolo) {
         // session w, all its pages; the first table entries load beside n_keys
         // (tab_read entries of every row are readable), not after it
@@ -415,7 +452,15 @@ decode_split_kernel(DecodeArgs a) {
         // one load: lane t holds phys[t]; lanes 0..3 the header
         const int32_t* rec = a.plan + plan_rec_off(a.n_sess) + (int64_t)w * kRec;
         tv = rec[lane];
-        const int hv = rec[kRecPages + (lane & 7)];
+        int hv = rec[kRecPages + (lane & 7)];
+        if constexpr (kSingle) {
+            // in flight while the record travels (issued after it, so the
+            // wait for the record below does not wait for them); the move
+            // keeps the compiler from sinking them below that wait
+            issue_new(0);
+            issue_q(0);
+            asm volatile("v_mov_b32 %0, %1" : "=v"(hv) : "v"(hv) : "memory");
+        }
         i = __builtin_amdgcn_readlane(hv, 0);
         if (i < 0) return;                       // idle workgroup (uniform)
         pa = __builtin_amdgcn_readlane(hv, 1);
@@ -514,35 +559,12 @@ decode_split_kernel(DecodeArgs a) {
         // (and the barrier behind it) would wait for the whole pair to arrive.
         const bool appends = (kRope || a.k_new) && pb == last_page + 1;
         const bool early = !(appends && pa + 2 * r + 1 >= last_page);
-        // Every wave issues the same loads in the same order, whatever its
-        // role, so that the compiler's waits count exactly: a wave without a
-        // use for one reads a valid line and drops it.
         const int phys_last = table[last_page];     // the appended token's page (may lie past the slice register)
         static_assert(KVW / 8 <= THREADS, "one 16-byte piece of the appended row per thread");
-        // (a kv-split workgroup appends its own kv head's part of the row)
-        constexpr int kAppW = kKvSplit ? HD : KVW;      // halfs of the row this workgroup appends
-        const int app_off = kKvSplit ? kvh * HD : 0;
-        const bool app_thread = !kRope && appends && tid < kAppW / 8;
-        u4 knew, vnew;
-        {
-            const uint16_t* ks = a.k_new ? a.k_new : reinterpret_cast<const uint16_t*>(a.q);
-            const uint16_t* vs = a.v_new ? a.v_new : reinterpret_cast<const uint16_t*>(a.q);
-            const int64_t src = app_thread ? (int64_t)i * KVW + app_off + 8 * tid : 0;
-            knew = *reinterpret_cast<const u4*>(ks + src);
-            vnew = *reinterpret_cast<const u4*>(vs + src);
-        }
-        f4 qraw[8];
-        const bool qreal = c < G;
-        {
-            // the converting wave of each kv head (r == 0) reads its rows; the others one line
-            const int64_t qoff = r == 0 ? ((int64_t)i * NH + kvh * G + (qreal ? c : 0)) * HD + 8 * g : (int64_t)i * NH * HD;
-            const int step = r == 0 ? 1 : 0;
-            const float* qp = a.q + qoff;
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                qraw[2 * ks] = *reinterpret_cast<const f4*>(qp + step * (32 * ks));
-                qraw[2 * ks + 1] = *reinterpret_cast<const f4*>(qp + step * (32 * ks + 4));
-            }
+        const bool app_thread = app_lane && appends;
+        if constexpr (!kSingle) {
+            issue_new(i);
+            issue_q(i);
         }
         // fused RoPE: the cos/sin row of position n_keys - 1 for this lane's q
         // dims, and this thread's piece of the new k (one NeoX pair) and v
@@ -679,7 +701,10 @@ decode_split_kernel(DecodeArgs a) {
             const bool tail = !two || (((pg0 + 2) << kKvBlockShift) > n_keys);
 
             // S = K . Q^T  (C layout: lane (g,c) holds keys 4g+i of head c)
+            // hi and lo products in separate accumulators: four chains of four
+            // dependent MFMAs instead of two of eight
             f4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+            f4 t0 = {0.f, 0.f, 0.f, 0.f}, t1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const h8 ka = __builtin_bit_cast(h8, k_operand(cur.k0, ks));
@@ -688,9 +713,11 @@ decode_split_kernel(DecodeArgs a) {
                 const h8 qlo = __builtin_bit_cast(h8, s_q[kvh][ks][1][lane]);
                 s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qhi, s0, 0, 0, 0);
                 s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qhi, s1, 0, 0, 0);
-                s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo, s0, 0, 0, 0);
-                s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qlo, s1, 0, 0, 0);
+                t0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qlo, t0, 0, 0, 0);
+                t1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qlo, t1, 0, 0, 0);
             }
+            s0 += t0;
+            s1 += t1;
             float s[8];
             bool ok[8];
 #pragma unroll
@@ -710,25 +737,36 @@ decode_split_kernel(DecodeArgs a) {
                 for (int j = 0; j < 8; ++j)
                     if (!ok[j]) cur.v[j] = u4{0u, 0u, 0u, 0u};   // unwritten slots may hold NaN bits
             }
-            float bm = -INFINITY;
+            // Lazy max: the running max m of a head only moves when a score
+            // exceeds it by more than kLazy (log2 units), so weights stay
+            // <= 2^kLazy (exact in the hi/lo fp16 split) and the common pair
+            // needs one lane-local test and a ballot -- no cross-lane max, no
+            // rescale of the accumulators.  The first pair (m = -inf) always
+            // moves it.
+            float lm = -INFINITY;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) bm = ok[j] ? fmaxf(bm, s[j]) : bm;
-            bm = fmaxf(bm, shfl_xor_f(bm, 16));
-            bm = fmaxf(bm, shfl_xor_f(bm, 32));
-            const float mn = fmaxf(m, bm);
-            const float corr = exp2f(m - mn);
+            for (int j = 0; j < 8; ++j) lm = ok[j] ? fmaxf(lm, s[j]) : lm;
+            if (__builtin_amdgcn_ballot_w64(lm > m + kLazy)) {
+                float bm = fmaxf(lm, shfl_xor_f(lm, 16));
+                bm = fmaxf(bm, shfl_xor_f(bm, 32));
+                const float mn = fmaxf(m, bm);
+                const float corr = __builtin_amdgcn_exp2f(m - mn);   // m = -inf: 0
+                lsum *= corr;
+#pragma unroll
+                for (int cb = 0; cb < 8; ++cb) acc[cb] *= corr;
+                m = mn;
+            }
             float ps = 0.f;
             h8 phi, plo;
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const float p = ok[j] ? exp2f(s[j] - mn) : 0.f;
+                const float p = ok[j] ? __builtin_amdgcn_exp2f(s[j] - m) : 0.f;
                 ps += p;
                 const _Float16 h = (_Float16)p;
                 phi[j] = h;
                 plo[j] = (_Float16)(p - (float)h);
             }
-            lsum = fmaf(lsum, corr, ps);
-            m = mn;
+            lsum += ps;
 
             // O^T += V^T . P^T   (A: lane (g,c) holds V[kappa(g,j)][8c + cb], j = 0..7)
 #pragma unroll
@@ -741,7 +779,6 @@ decode_split_kernel(DecodeArgs a) {
                 for (int u = 0; u < 4; ++u)
                     vw[u] = __builtin_amdgcn_perm(cur.v[2 * u + 1][cb >> 1], cur.v[2 * u][cb >> 1], sel);
                 const h8 va = __builtin_bit_cast(h8, vw);
-                acc[cb] *= corr;
                 acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, phi, acc[cb], 0, 0, 0);
                 acc[cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, plo, acc[cb], 0, 0, 0);
             }
@@ -1300,8 +1337,11 @@ int batch_workgroups() {
 void launch_split(const DecodeArgs& a, int n_sess, hipStream_t st) {
     const dim3 grid = a.kv_split ? dim3(NKV, a.gw + n_sess)
                                  : dim3(a.plan ? split_slots(n_sess, a.gw) : a.gw + n_sess);
+    const bool single = a.plan && n_sess == 1;
     if (a.kv_split) hipLaunchKernelGGL((decode_split_kernel<false, true>), grid, dim3(THREADS), 0, st, a);
+    else if (a.cs && single) hipLaunchKernelGGL((decode_split_kernel<true, false, false, true>), grid, dim3(THREADS), 0, st, a);
     else if (a.cs) hipLaunchKernelGGL((decode_split_kernel<true, false>), grid, dim3(THREADS), 0, st, a);
+    else if (single) hipLaunchKernelGGL((decode_split_kernel<false, false, false, true>), grid, dim3(THREADS), 0, st, a);
     else hipLaunchKernelGGL((decode_split_kernel<false, false>), grid, dim3(THREADS), 0, st, a);
     NOVA_LAUNCHED();
 }

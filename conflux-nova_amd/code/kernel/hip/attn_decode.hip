@@ -377,6 +377,12 @@ __global__ void __launch_bounds__(THREADS)
 decode_split_kernel(DecodeArgs a) {
     static_assert(!kSolo || kKvSplit, "solo workgroups serve one kv head");
     static_assert(!kSingle || !kKvSplit, "single-session launches use the planned grid");
+    // two page pairs in flight per wave (the next pair's loads go out before
+    // this pair's arithmetic): solo workgroups only.  The split grid is
+    // slower with it (config 2 split kernel 25.7-26.3 vs 23.8-24.8 us, 256
+    // VGPRs with 2-4 spilled; the per-pair waits counted exactly): its 8 waves
+    // per CU already keep enough of the chip's bytes in flight.
+    constexpr bool kDB = kSolo;
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];
     __shared__ float s_acc[(R > 1 || kKvSplit) ? WAVES : 1][G][HD];
@@ -386,7 +392,7 @@ decode_split_kernel(DecodeArgs a) {
 
     const int tid = threadIdx.x;
     // solo: the wave index (and the pair loop) kept in scalar registers
-    const int wave = kSolo ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
+    const int wave = kDB ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int lane = tid & 63;
     const int g = lane >> 4;      // 0..3
     const int c = lane & 15;      // 0..15
@@ -500,13 +506,14 @@ decode_split_kernel(DecodeArgs a) {
         int tchunk = 0;
         auto phys_of = [&](int pg) -> int {
             const int rel = pg - pa;
-            if constexpr (kSolo) {
-                // the first 128 entries sit in tv, tv2; later pages come one at
-                // a time through the scalar cache.  No vector load in the pair
-                // loop but the pairs', so the compiler's waits count exactly and
-                // the prefetched pair stays in flight during the arithmetic.
+            if constexpr (kDB) {
+                // the first 64 (solo: 128) entries sit in tv (, tv2); later
+                // pages come one at a time through the scalar cache.  No vector
+                // load in the pair loop but the pairs', so the compiler's waits
+                // count exactly and the prefetched pair stays in flight during
+                // the arithmetic.
                 if (rel < 64) return __builtin_amdgcn_readlane(tv, rel);
-                if (rel < 128) return __builtin_amdgcn_readlane(tv2, rel - 64);
+                if (kSolo && rel < 128) return __builtin_amdgcn_readlane(tv2, rel - 64);
                 return *(const __attribute__((address_space(4))) int32_t*)(uintptr_t)(table + pg);
             }
             if ((rel >> 6) != tchunk) {          // rare: ranges longer than 64 pages
@@ -788,10 +795,10 @@ decode_split_kernel(DecodeArgs a) {
         // overlap each other's latency (measured: a second pair prefetched
         // before the query conversion only delays the query rows further
         // behind the chip's first burst, 0.778 -> 0.791 ms per config-2 step)
-        if constexpr (kSolo) {
-            // one CU streams the whole session's head: the next pair's loads
-            // go out before this pair's arithmetic (two pairs in flight per
-            // wave), so the CU's stream does not stop at every pair
+        if constexpr (kDB) {
+            // the next pair's loads go out before this pair's arithmetic (two
+            // pairs in flight per wave), so the wave's stream does not stop at
+            // every pair
             // Two register sets take turns (no copy between them: a copy would
             // wait for the prefetch to land).
             if (!early && r < npairs) load_pair(std::false_type{}, r, cur);

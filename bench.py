@@ -207,9 +207,10 @@ class DecodeWorkload:
                                            self.nb, self.ws.ptr, s)
 
         # contiguous floor: the layer's algorithmic bytes as one contiguous
-        # non-temporal read by one 512-thread workgroup per CU (no pages, no
-        # table); layers take disjoint ranges (K pool for the first half of
-        # the layers, V pool for the rest), so nothing is read twice per step
+        # non-temporal grid-stride read by two 256-thread workgroups per CU
+        # (no pages, no table; the fastest streaming shape measured); layers
+        # take disjoint ranges (K pool for the first half of the layers, V
+        # pool for the rest), so nothing is read twice per step
         half = (L + 1) // 2
         nbytes = min(self.bytes_per_step() // L, nv.n_layers * self.layer_halves * 2 // half) // 16 * 16
         self.contig_bytes = nbytes
@@ -218,7 +219,7 @@ class DecodeWorkload:
 
         def contig(l):
             src = (self.k.ptr if l < half else self.v.ptr) + (l % half) * nbytes
-            nv.testkit_stream_read(src, nbytes, cus, sink.ptr, s)
+            nv.testkit_stream_read(src, nbytes, 2 * cus, sink.ptr, s)
 
         out = {}
         for name, fn in (("pair", self.launch_layer), ("split", split_only), ("floor", floor),
@@ -429,7 +430,7 @@ def run_decode(args, model, ctx, workload_name, metric_cfg, cpu_scale_note):
                       "(testkit_attn_decode_split_only), the split + combine pair "
                       "(launch_attn_decode_paged_planned) and the stream floor (testkit_decode_stream_floor: "
                       "the split grid reading the same pages with the same loads, no arithmetic), the contiguous "
-                      "floor (testkit_stream_read: the same bytes as one contiguous read, one workgroup per CU); "
+                      "floor (testkit_stream_read: the same bytes as one contiguous grid-stride read, two workgroups per CU); "
                       "step_frac = the timed step incl. the plan kernel"}
     # the one-launch solo path (one CU per session and kv head): timed where
     # its sessions are short enough to finish in minutes at this step count

@@ -27,9 +27,10 @@ void testkit_fill_normal_f16(uint16_t* p, uint64_t n, uint64_t seed, float scale
 void testkit_copy(void* dst, const void* src, uint64_t bytes, nova_stream_t s);
 
 /* Contiguous streaming read of `bytes` (a multiple of 16) by `workgroups`
- * workgroups of 512 threads, non-temporal 16-byte loads with 16 per lane in flight, one sink word per
- * thread into `sink` (workgroups * 512 uint32): the HBM floor of reading a
- * layer's K/V bytes with no paging at all. */
+ * workgroups of 256 threads, grid-stride non-temporal 16-byte loads with 4
+ * per lane in flight, one sink word per thread into `sink` (workgroups * 256
+ * uint32): the HBM floor of reading a layer's K/V bytes with no paging at
+ * all (two workgroups per CU is the fastest shape measured). */
 void testkit_stream_read(const void* src, uint64_t bytes, int workgroups, uint32_t* sink, nova_stream_t s);
 
 /* Only the split kernel of launch_attn_decode_paged_planned (partials

@@ -405,3 +405,67 @@ def test_decode_batch_uneven_ranges_1p5b(n_keys, oracle):
         ref = oracle.attn_decode_paged("qwen25_1p5b", np.ascontiguousarray(q[i]), fx.hk, fx.hv, tables[i], 0,
                                        fx.nb, int(n_keys[i]))
         assert_close(got[i], ref, what=f"session {i} n_keys={n_keys[i]}")
+
+
+@pytest.mark.parametrize("model", ["qwen25_1p5b", "qwen25_7b", "qwen25_14b"])
+@pytest.mark.parametrize("n_keys", [1, 17, 1025, 3000])
+def test_decode_batch_one_session(model, n_keys, oracle):
+    """A batched call with one session takes the single-session split kernel
+    (query and new-token rows loaded beside the plan record): fused append
+    bit-exact, output against the oracle and f64, repeated calls identical."""
+    import nova_amd
+    nova = nova_amd.load(model)
+    rng = np.random.default_rng(n_keys)
+    pages = (n_keys + 15) // 16
+    print(f"[case] decode one session model={model} n_keys={n_keys}", flush=True)
+    fx = PagedFixture(nova, nb=pages + 4, layer=LAYER, seed=n_keys + 3)
+    tables = fx.tables(1, pages)
+    q = rng.standard_normal((1, nova.nh, nova.hd)).astype(np.float32)
+    k_new = f16(rng, (1, nova.nkv, nova.hd))
+    v_new = f16(rng, (1, nova.nkv, nova.hd))
+    got = _batch(nova, fx, q, tables, np.array([n_keys], np.int32), k_new, v_new)
+    hk, hv = fx.hk.copy(), fx.hv.copy()
+    oracle.kv_store_paged(model, hk, hv, tables[0], 0, fx.nb, 1, n_keys - 1, np.ascontiguousarray(k_new[0]),
+                          np.ascontiguousarray(v_new[0]))
+    gk, gv = fx.pull()
+    assert np.array_equal(gk, hk) and np.array_equal(gv, hv), "fused append not bit-exact"
+    ref = oracle.attn_decode_paged(model, np.ascontiguousarray(q[0]), hk, hv, tables[0], 0, fx.nb, n_keys)
+    err = assert_close(got[0], ref, what=f"{model} one session n_keys={n_keys}")
+    err64 = float(np.abs(got[0] - _decode_f64(q[0], hk, hv, tables[0], n_keys, nova.group)).max())
+    print(f"  max|gpu-oracle|={err:.3e} max|gpu-f64|={err64:.3e}")
+    assert err64 < 1e-4
+
+
+@pytest.mark.parametrize("model", ["qwen25_1p5b", "qwen25_7b"])
+def test_decode_rope_one_session(model, oracle):
+    """launch_attn_decode_paged_rope_batch with one session (the single-session
+    split kernel with RoPE fused): rows bit-exact, output within tolerance."""
+    import nova_amd
+    nova = nova_amd.load(model)
+    rng = np.random.default_rng(31)
+    n_keys = np.array([777], np.int32)
+    pages = int((n_keys[0] + 15) // 16)
+    fx = PagedFixture(nova, nb=pages + 4, layer=LAYER, seed=12)
+    tables = fx.tables(1, pages)
+    half = nova.hd // 2
+    dcs, dsn = nova.alloc(4096 * half * 4), nova.alloc(4096 * half * 4)
+    nova.launch_rope_table(dcs.ptr, dsn.ptr, None)
+    nova.dev_sync()
+    cs, sn = dcs.numpy((4096, half), np.float32), dsn.numpy((4096, half), np.float32)
+    q = rng.standard_normal((1, nova.nh, nova.hd)).astype(np.float32)
+    k = rng.standard_normal((1, nova.nkv, nova.hd)).astype(np.float32)
+    v = rng.standard_normal((1, nova.nkv, nova.hd)).astype(np.float32)
+    ws = nova.alloc(nova.attn_decode_batch_workspace_bytes(1))
+    dq, dk, dv, dt, dn = nova.upload(q), nova.upload(k), nova.upload(v), nova.upload(tables), nova.upload(n_keys)
+    do = nova.alloc(q.nbytes)
+    nova.launch_attn_decode_paged_rope_batch(dq.ptr, dk.ptr, dv.ptr, dcs.ptr, dsn.ptr, fx.k.ptr, fx.v.ptr, dt.ptr,
+                                             pages, dn.ptr, 1, LAYER, fx.nb, do.ptr, ws.ptr, None)
+    nova.dev_sync()
+    got = do.numpy(q.shape, np.float32)
+    hk, hv = fx.hk.copy(), fx.hv.copy()
+    rq = oracle.rope_kv_store_paged(model, q, k, v, cs, sn, hk, hv, np.ascontiguousarray(tables[0]), 0, fx.nb,
+                                    int(n_keys[0]) - 1)[0]
+    gk, gv = fx.pull()
+    assert np.array_equal(gk, hk) and np.array_equal(gv, hv), "fused rope + append not bit-exact"
+    ref = oracle.attn_decode_paged(model, np.ascontiguousarray(rq), hk, hv, tables[0], 0, fx.nb, int(n_keys[0]))
+    assert_close(got[0], ref, what=f"{model} rope one session")

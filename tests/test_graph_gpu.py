@@ -40,6 +40,14 @@ def _replays(nova, s, run, read, n=4):
     return eager, outs
 
 
+def _fill_layers(fx, layers):
+    """seeded fp16 pages in every layer a test reads (the fixture fills one)"""
+    for layer in layers:
+        off = layer * fx.nb * fx.page_halves * 2
+        fx.nova.dev_upload(fx.k.ptr + off, fx.hk.ctypes.data, fx.hk.nbytes)
+        fx.nova.dev_upload(fx.v.ptr + off, fx.hv.ctypes.data, fx.hv.nbytes)
+
+
 def test_decode_step_graph(nova7):
     """plan + fused-append decode of three layers for 6 ragged sessions"""
     nova = nova7
@@ -196,4 +204,86 @@ def test_gemv4_mfma_graph(nova7):
     eager, reps = _replays(nova, s, run, lambda: out4.numpy((4 * rows,), np.float32))
     assert np.all(np.isfinite(eager))
     for r, got in enumerate(reps):
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"
+
+
+def test_reference_call_pattern_graph(nova7):
+    """the reference's per-session calls (launch_kv_store_paged, then
+    launch_attn_decode_paged) for sessions on both sides of the one-launch
+    short-context path (<= 40 pages) and the split + combine pair, two layers"""
+    nova = nova7
+    print("[case] graph reference call pattern", flush=True)
+    n_keys = np.array([1, 17, 640, 641, 1500], np.int32)      # 1, 2, 40, 41, 94 pages
+    n = len(n_keys)
+    pages = int((n_keys.max() + 15) // 16)
+    fx = PagedFixture(nova, nb=n * pages + 3, layer=LAYERS[0], seed=21)
+    tables = fx.tables(n, pages)
+    rng = np.random.default_rng(9)
+    layers = LAYERS[:2]
+    _fill_layers(fx, layers)
+    q = nova.upload(rng.standard_normal((len(layers), n, nova.nh, nova.hd)).astype(np.float32))
+    kn = nova.upload(f16(rng, (len(layers), n, nova.nkv, nova.hd)))
+    vn = nova.upload(f16(rng, (len(layers), n, nova.nkv, nova.hd)))
+    o = nova.upload(np.full((len(layers), n, nova.nh, nova.hd), np.nan, np.float32))
+    dts = [nova.upload(np.ascontiguousarray(tables[i])) for i in range(n)]
+    scratch = [nova.alloc(nova.nh * 32 * (nova.hd + 2) * 4) for _ in range(n)]
+    s = nova.dev_stream_create()
+    qrow, kvrow = nova.nh * nova.hd, nova.kvw
+
+    def run():
+        for li, layer in enumerate(layers):
+            for i in range(n):
+                r = li * n + i
+                nova.launch_kv_store_paged(fx.k.ptr, fx.v.ptr, dts[i].ptr, layer, fx.nb, 1, int(n_keys[i]) - 1,
+                                           kn.ptr + r * kvrow * 2, vn.ptr + r * kvrow * 2, s)
+                nova.launch_attn_decode_paged(q.ptr + r * qrow * 4, fx.k.ptr, fx.v.ptr, dts[i].ptr, layer, fx.nb,
+                                              int(n_keys[i]), o.ptr + r * qrow * 4, scratch[i].ptr, s)
+
+    eager, outs = _replays(nova, s, run, lambda: o.numpy((len(layers), n, nova.nh, nova.hd), np.float32))
+    assert np.all(np.isfinite(eager))
+    for r, got in enumerate(outs):
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"
+
+
+def test_solo_step_graph(nova7):
+    """the one-launch decode (fused append, then the RoPE-fused form) of two
+    layers for ragged sessions, including an empty one"""
+    nova = nova7
+    print("[case] graph solo decode step", flush=True)
+    n_keys = np.array([300, 0, 1, 129, 33], np.int32)
+    n = len(n_keys)
+    pages = int((n_keys.max() + 15) // 16)
+    fx = PagedFixture(nova, nb=n * pages + 3, layer=LAYERS[0], seed=23)
+    tables = fx.tables(n, pages)
+    rng = np.random.default_rng(13)
+    layers = LAYERS[:2]
+    _fill_layers(fx, list(layers) + [layer + 1 for layer in layers])
+    q = nova.upload(rng.standard_normal((len(layers), n, nova.nh, nova.hd)).astype(np.float32))
+    kn = nova.upload(f16(rng, (len(layers), n, nova.nkv, nova.hd)))
+    vn = nova.upload(f16(rng, (len(layers), n, nova.nkv, nova.hd)))
+    k32 = nova.upload(rng.standard_normal((len(layers), n, nova.nkv, nova.hd)).astype(np.float32))
+    v32 = nova.upload(rng.standard_normal((len(layers), n, nova.nkv, nova.hd)).astype(np.float32))
+    cs, sn = nova.alloc(4096 * (nova.hd // 2) * 4), nova.alloc(4096 * (nova.hd // 2) * 4)
+    nova.launch_rope_table(cs.ptr, sn.ptr, None)
+    o = nova.upload(np.full((2, len(layers), n, nova.nh, nova.hd), np.nan, np.float32))
+    dt, dn = nova.upload(tables), nova.upload(n_keys)
+    s = nova.dev_stream_create()
+    qs, kvs = n * nova.nh * nova.hd, n * nova.kvw
+    ostride = len(layers) * qs
+
+    def run():
+        for li, layer in enumerate(layers):
+            nova.launch_attn_decode_paged_solo(q.ptr + li * qs * 4, fx.k.ptr, fx.v.ptr, dt.ptr, pages, dn.ptr, n,
+                                               layer, fx.nb, kn.ptr + li * kvs * 2, vn.ptr + li * kvs * 2,
+                                               o.ptr + li * qs * 4, s)
+        for li, layer in enumerate(layers):
+            nova.launch_attn_decode_paged_rope_solo(q.ptr + li * qs * 4, k32.ptr + li * kvs * 4,
+                                                    v32.ptr + li * kvs * 4, cs.ptr, sn.ptr, fx.k.ptr, fx.v.ptr,
+                                                    dt.ptr, pages, dn.ptr, n, layer + 1, fx.nb,
+                                                    o.ptr + (ostride + li * qs) * 4, s)
+
+    eager, outs = _replays(nova, s, run, lambda: o.numpy((2, len(layers), n, nova.nh, nova.hd), np.float32))
+    assert np.all(np.isfinite(eager))
+    assert np.all(eager[:, :, 1] == 0), "a session without keys gets zero rows"
+    for r, got in enumerate(outs):
         assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"

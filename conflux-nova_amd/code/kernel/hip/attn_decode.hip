@@ -188,11 +188,17 @@ __device__ __forceinline__ float shfl_xor_f(float v, int m) { return __shfl_xor(
 // loads 0.834-0.841 -> 0.826 ms (config 4: 6.21 -> 6.37-6.55 TB/s).  K
 // loaded the MFMA's way (64 B of 16 rows per instruction, the other half of
 // each line by the next one) is slower non-temporal: 0.97 ms.
-__device__ __forceinline__ u4 ld16(const char* base, uint32_t off) {
-    return *reinterpret_cast<const u4*>(base + off);
+// Each page is a buffer resource: the loads take the page base in SGPRs and a
+// 32-bit lane offset with an immediate, instead of a 64-bit VGPR address per
+// load (the double-buffered solo loop: 254 -> 217 VGPRs, and its prefetch no
+// longer waits on address registers still being loaded).  num_records bounds
+// every load to its page; num_records = 0 makes a load return zero without a
+// memory access (a prefetch slot with no pair left).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const char* base, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), 0, bytes, 0x00020000);
 }
-__device__ __forceinline__ u4 ld16_nt(const char* base, uint32_t off) {
-    return __builtin_nontemporal_load(reinterpret_cast<const u4*>(base + off));
+__device__ __forceinline__ u4 ldb16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));   // aux 2: nt
 }
 
 #ifdef NOVA_DECODE_TRACE
@@ -528,33 +534,31 @@ decode_split_kernel(DecodeArgs a) {
         // kFirst: a wave's first pair (pages < 16 into the range) takes its pages
         // straight from the slice register, with no reload branch: a reload's
         // load would make the first pair's issue wait for every load before it
-        // live == false: the same 16 loads, all lanes on the layer's first
-        // 16 bytes (one cached line), for a prefetch slot with no pair left --
-        // a load under a branch would make the compiler drain every load in
-        // flight before the next use of any of them
+        // live == false: the same 16 loads with an empty resource (they
+        // return zero, no memory access), for a prefetch slot with no pair
+        // left -- a load under a branch would make the compiler drain every
+        // load in flight before the next use of any of them
         auto load_pair = [&](auto first_tag, int qp, PairRegs& pr, bool live = true) {
             constexpr bool kFirst = decltype(first_tag)::value;
             const int pg0 = pa + 2 * qp;
             const int pg1 = pg0 + 1 < pb ? pg0 + 1 : pg0;   // a lone last page loads itself twice
             const int ph0 = kFirst ? __builtin_amdgcn_readlane(tv, pg0 - pa) : phys_of(pg0);
             const int ph1 = kFirst ? __builtin_amdgcn_readlane(tv, pg1 - pa) : phys_of(pg1);
-            const int64_t b0 = (layer_page0 + (live ? ph0 : 0)) * kPageBytes;
-            const int64_t b1 = (layer_page0 + (live ? ph1 : 0)) * kPageBytes;
-            const uint32_t lm = live ? ~0u : 0u;
-            const char* k0 = pk + b0;
-            const char* k1 = pk + b1;
-            const char* v0 = pv + b0;
-            const char* v1 = pv + b1;
+            const int64_t b0 = (layer_page0 + ph0) * kPageBytes;
+            const int64_t b1 = (layer_page0 + ph1) * kPageBytes;
+            const int nr = live ? (int)kPageBytes : 0;
+            const auto rk0 = page_rsrc(pk + b0, nr), rk1 = page_rsrc(pk + b1, nr);
+            const auto rv0 = page_rsrc(pv + b0, nr), rv1 = page_rsrc(pv + b1, nr);
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
-                const uint32_t o = (koff + (ks & 1) * 8 * kRowBytes + (ks >> 1) * 128) & lm;
-                pr.k0[ks] = ld16_nt(k0, o);
-                pr.k1[ks] = ld16_nt(k1, o);
+                const uint32_t o = koff + (ks & 1) * 8 * kRowBytes + (ks >> 1) * 128;
+                pr.k0[ks] = ldb16_nt(rk0, o);
+                pr.k1[ks] = ldb16_nt(rk1, o);
             }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                pr.v[j] = ld16_nt(v0, voff[j] & lm);
-                pr.v[4 + j] = ld16_nt(v1, voff[j] & lm);
+                pr.v[j] = ldb16_nt(rv0, voff[j]);
+                pr.v[4 + j] = ldb16_nt(rv1, voff[j]);
             }
         };
 
@@ -806,10 +810,14 @@ decode_split_kernel(DecodeArgs a) {
             for (int qp = r; qp < npairs; qp += 2 * RS) {
                 const bool m1 = qp + RS < npairs;
                 load_pair(std::false_type{}, m1 ? qp + RS : qp, alt, m1);
+                // issued before the waits for this pair (the counter drains in
+                // issue order): without the pin the scheduler sinks them below
+                __builtin_amdgcn_sched_barrier(0);
                 compute_pair(qp, cur);
                 if (!m1) break;
                 const bool m2 = qp + 2 * RS < npairs;
                 load_pair(std::false_type{}, m2 ? qp + 2 * RS : qp, cur, m2);
+                __builtin_amdgcn_sched_barrier(0);
                 compute_pair(qp + RS, alt);
             }
         } else {
@@ -1062,17 +1070,19 @@ decode_stream_floor_kernel(DecodeArgs a) {
         const int pg1 = pg0 + 1 < pb ? pg0 + 1 : pg0;
         const int64_t b0 = (layer_page0 + phys_of(pg0)) * kPageBytes;
         const int64_t b1 = (layer_page0 + phys_of(pg1)) * kPageBytes;
+        const auto rk0 = page_rsrc(pk + b0, (int)kPageBytes), rk1 = page_rsrc(pk + b1, (int)kPageBytes);
+        const auto rv0 = page_rsrc(pv + b0, (int)kPageBytes), rv1 = page_rsrc(pv + b1, (int)kPageBytes);
         u4 x[16];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const uint32_t o = koff + (ks & 1) * 8 * kRowBytes + (ks >> 1) * 128;
-            x[ks] = ld16_nt(pk + b0, o);
-            x[4 + ks] = ld16_nt(pk + b1, o);
+            x[ks] = ldb16_nt(rk0, o);
+            x[4 + ks] = ldb16_nt(rk1, o);
         }
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-            x[8 + jj] = ld16_nt(pv + b0, voff[jj]);
-            x[12 + jj] = ld16_nt(pv + b1, voff[jj]);
+            x[8 + jj] = ldb16_nt(rv0, voff[jj]);
+            x[12 + jj] = ldb16_nt(rv1, voff[jj]);
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) sum += x[e];

@@ -385,9 +385,10 @@ decode_split_kernel(DecodeArgs a) {
     static_assert(!kSingle || !kKvSplit, "single-session launches use the planned grid");
     // two page pairs in flight per wave (the next pair's loads go out before
     // this pair's arithmetic): solo workgroups only.  The split grid is
-    // slower with it (config 2 split kernel 25.7-26.3 vs 23.8-24.8 us, 256
-    // VGPRs with 2-4 spilled; the per-pair waits counted exactly): its 8 waves
-    // per CU already keep enough of the chip's bytes in flight.
+    // slower with it even at 242 VGPRs with no spills and the prefetch in
+    // flight (config 2 split kernel 26.5-27.0 vs 23.6-24.6 us, config 1
+    // 8.0 vs 6.15 us, config 4 unchanged): its 8 waves per CU already keep
+    // enough of the chip's bytes in flight.
     constexpr bool kDB = kSolo;
     __shared__ float s_m[WAVES][16];
     __shared__ float s_l[WAVES][16];

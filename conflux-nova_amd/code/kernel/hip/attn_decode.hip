@@ -201,14 +201,6 @@ __device__ __forceinline__ u4 ldb16_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));   // aux 2: nt
 }
 
-#ifdef NOVA_DECODE_TRACE
-// per-workgroup timeline (development builds only): 8 x 64-bit per (layer, workgroup slot)
-__device__ uint64_t g_trace[64 * 512 * 8];
-#define TRACE(k) do { if ((threadIdx.x & 63) == 0 && blockIdx.x < 512) g_trace[((int64_t)(a.layer & 63) * 512 + blockIdx.x) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define TRACE(k) do {} while (0)
-#endif
-
 // Pages per workgroup: the even share ceil(T / gw), but at least kMinShare so
 // that small batches do not spread one or two pages per workgroup (each extra
 // workgroup costs a partial row and a combine term).  4 pages = one pair per
@@ -412,7 +404,6 @@ decode_split_kernel(DecodeArgs a) {
     const int r = kKvSplit ? wave : wave / NKV;
     constexpr int RS = kKvSplit ? WAVES : R;        // waves per kv head = pair stride
     const int w = kKvSplit ? (int)blockIdx.y : (int)blockIdx.x;
-    if (wave == 0) TRACE(0);
 
     int i, n_keys, pa, pb, tv, slot = w;        // slot: this workgroup's partial row index
     int tv2 = 0;                                 // solo: table entries 64..127
@@ -698,7 +689,6 @@ decode_split_kernel(DecodeArgs a) {
         }
         if (lane == 0) s_ready[wave] = 0;
         __syncthreads();
-        if (wave == 0) TRACE(1);
         const float qf = s_qf[kvh][c];
 
         float m = -INFINITY, lsum = 0.f;
@@ -825,10 +815,8 @@ decode_split_kernel(DecodeArgs a) {
             for (int qp = r; qp < npairs; qp += RS) {
                 if (qp != r || !early) load_pair(std::false_type{}, qp, cur);
                 compute_pair(qp, cur);
-                if (wave == 0 && qp == r) TRACE(2);
             }
         }
-        if (wave == 0) TRACE(3);
 
         lsum += shfl_xor_f(lsum, 16);
         lsum += shfl_xor_f(lsum, 32);
@@ -1020,10 +1008,6 @@ decode_split_kernel(DecodeArgs a) {
             }
         }
     }
-#ifdef NOVA_DECODE_TRACE
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    if (wave == 0) TRACE(4);
-#endif
 }
 
 #ifdef NOVA_TESTKIT
@@ -1109,12 +1093,6 @@ constexpr int kCombGroups = CT / (HD / 4);
 __global__ void __launch_bounds__(CT)
 decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     const int t = blockIdx.x;
-#ifdef NOVA_DECODE_TRACE
-#define CTRACE(k) do { if (threadIdx.x == 0 && blockIdx.x < 512) g_trace[((int64_t)(a.layer & 63) * 512 + blockIdx.x) * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define CTRACE(k) do {} while (0)
-#endif
-    CTRACE(5);
     int i, h;
     const int tid = threadIdx.x, g = tid / (HD / 4), q4 = tid - g * (HD / 4);
     __shared__ float s_m[kCombGroups], s_l[kCombGroups];
@@ -1129,10 +1107,6 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
         h = e.z >> 16;
         pt.pages = e.w;
         pt.sess = i;
-#ifdef NOVA_DECODE_TRACE
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        CTRACE(6);
-#endif
     } else {
         if (a.kv_split) {
             // single session: head kvh * G + m runs on a block whose XCD
@@ -1216,10 +1190,6 @@ decode_combine_kernel(DecodeArgs a, float* __restrict__ o) {
     }
     const float inv = Lx > 0.f ? 1.f / Lx : 0.f;
     *orow = Ax * inv;
-#ifdef NOVA_DECODE_TRACE
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    CTRACE(7);
-#endif
 }
 
 // Per-step plan: block w (< split_slots) writes the record of workgroup slot w;
@@ -1463,9 +1433,6 @@ using namespace nova;
 
 extern "C" {
 
-#ifdef NOVA_DECODE_TRACE
-void nova_decode_trace_copy(void* host) { NOVA_HIP(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), sizeof(g_trace))); }
-#endif
 
 #ifndef NOVA_TESTKIT
 

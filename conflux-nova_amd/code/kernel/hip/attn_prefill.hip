@@ -309,9 +309,6 @@ __device__ __forceinline__ uint32_t swz_v(int row, int chunk) {
     return (uint32_t)(row * ROWB + ((chunk ^ (2 * (row & 7))) << 4));
 }
 
-#ifdef NOVA_PREFILL_TRACE
-__device__ uint64_t g_pf_trace[4096 * 4];
-#endif
 
 // NB: 16-column blocks per wave.  KS: key groups -- KS groups of 4 waves
 // share the workgroup's columns; group k takes the key tiles KS*i + k with
@@ -346,9 +343,6 @@ prefill_kernel(PrefillArgs a) {
     const int kvh = xcd / kXcdPerHead;
     const int rank = ((int)blockIdx.x / kXcd) * kXcdPerHead + xcd % kXcdPerHead;
     if (rank >= N) return;                                  // grid padding (uniform)
-#ifdef NOVA_PREFILL_TRACE
-    const uint64_t t_start = __builtin_amdgcn_s_memrealtime();
-#endif
     int item;
     if (a.n_sess == 1 || N > kRankMax) item = (rank / n_cg) * n_cg + (n_cg - 1 - rank % n_cg);
     else item = lpt_item<NT>(a, rank, n_cg, n_cols, COLS_WG, reinterpret_cast<int*>(&s_kv[0][0][0]));
@@ -679,10 +673,6 @@ prefill_kernel(PrefillArgs a) {
         if (ahead) tile_barrier<LOADS>();
         else tile_barrier<0>();
     };
-#ifdef NOVA_PREFILL_PHASE
-    // development: offset the phase of alternate workgroups by about half a tile
-    if (blockIdx.x & NOVA_PREFILL_PHASE) __builtin_amdgcn_s_sleep(12);
-#endif
     for (int i = 0; i < n_steps; i += NBUF) {               // unrolled: buffers and score registers rotate
         step(std::integral_constant<int, 0>{}, i, sa0, sa1, sb0, sb1);
         if (i + 1 < n_steps) step(std::integral_constant<int, 1>{}, i + 1, sb0, sb1, sa0, sa1);
@@ -738,23 +728,6 @@ prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int cb = 0; cb < 8; ++cb) *reinterpret_cast<f4*>(op + 16 * cb + 4 * g) = acc[b][cb] * inv;
     }
-#ifdef NOVA_PREFILL_TRACE
-    // development builds: per-workgroup start, end, hardware ids and key tiles
-    if constexpr (KS == 1) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (tid == 0 && blockIdx.x < 4096) {
-            unsigned hw, xcc;
-            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw));
-            asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
-            uint64_t* tr = g_pf_trace + (int64_t)blockIdx.x * 4;
-            tr[0] = t_start;
-            tr[1] = __builtin_amdgcn_s_memrealtime();
-            tr[2] = hw;
-            tr[3] = ((uint64_t)xcc << 32) | (uint32_t)n_tiles;
-        }
-    }
-#endif
 }
 
 int compute_units() {
@@ -807,9 +780,6 @@ using namespace nova;
 
 extern "C" {
 
-#ifdef NOVA_PREFILL_TRACE
-void nova_prefill_trace_copy(void* host) { NOVA_HIP(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_pf_trace), sizeof(g_pf_trace))); }
-#endif
 
 void launch_attn_prefill_paged(const float* q, const uint16_t* pool_k, const uint16_t* pool_v,
                                const int32_t* table, int layer, int nb, int n_q, int n_past, float* o,

@@ -144,7 +144,7 @@ def random_trace(api, seed, n_slices, ctx, n_ops):
     return {"seed": seed, "n_slices": n_slices, "ctx": ctx, "ops": ops}
 
 
-def survey_probe(api):
+def fork_cow_probe(api):
     """init(3,64); acquire A, B; attach_prefix(B, A, 20); cow_slice(B, 20)"""
     h = api.new(3, 64)
     a, b = api.acquire(h), api.acquire(h)
@@ -250,7 +250,7 @@ def main():
     traces = [random_trace(pool, seed, ns, ctx, 60) for seed, ns, ctx in
               ((1, 3, 64), (2, 4, 80), (3, 5, 48), (4, 2, 100), (5, 6, 33))]
     (HERE / "pool_traces.json").write_text(json.dumps(
-        {"survey_probe": survey_probe(pool), "traces": traces, "fork": fork_scenario(pool)}))
+        {"fork_cow_probe": fork_cow_probe(pool), "traces": traces, "fork": fork_scenario(pool)}))
     (HERE / "registry.json").write_text(json.dumps(registry_fixture(ref)))
     for model in ("qwen25_7b", "qwen25_1p5b"):
         np.savez_compressed(HERE / f"attn_{model}.npz", **attn_fixture(ref, model))

@@ -26,8 +26,8 @@ def prod_pool(nova7):
     return PoolAPI(nova7.lib, "nova_kvpool_", True)
 
 
-def test_pool_survey_probe(prod_pool):
-    replay_probe(prod_pool, load_traces()["survey_probe"])
+def test_pool_fork_cow_probe(prod_pool):
+    replay_probe(prod_pool, load_traces()["fork_cow_probe"])
 
 
 @pytest.mark.parametrize("k", range(5))

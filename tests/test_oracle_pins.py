@@ -53,8 +53,8 @@ def test_kv_block_fold_by_hand(oracle):
     assert oracle.kv_hash_ids(ids) == w[0]
 
 
-def test_pool_survey_probe(oracle):
-    replay_probe(oracle.pool, load_traces()["survey_probe"])
+def test_pool_fork_cow_probe(oracle):
+    replay_probe(oracle.pool, load_traces()["fork_cow_probe"])
 
 
 @pytest.mark.parametrize("k", range(5))

@@ -145,6 +145,38 @@ def test_prefill_layer_graph(nova7):
         assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"
 
 
+def test_prefill_single_session_graph(nova7):
+    """the reference's per-session prefill calls (launch_kv_store_paged, then
+    launch_attn_prefill_paged: the 64-column, two-key-group kernel) for three
+    sessions, one of them with no prefix"""
+    nova = nova7
+    print("[case] graph single-session prefill", flush=True)
+    n_past = [0, 500, 1700]
+    n, n_q = len(n_past), 130
+    pages = (max(n_past) + n_q + 15) // 16
+    fx = PagedFixture(nova, nb=n * pages + 3, layer=LAYERS[1], seed=15)
+    tables = fx.tables(n, pages)
+    rng = np.random.default_rng(8)
+    q = nova.upload(rng.standard_normal((n, n_q, nova.nh, nova.hd)).astype(np.float32))
+    kc = nova.upload(f16(rng, (n, n_q, nova.nkv, nova.hd)))
+    vc = nova.upload(f16(rng, (n, n_q, nova.nkv, nova.hd)))
+    o = nova.upload(np.full((n, n_q, nova.nh, nova.hd), np.nan, np.float32))
+    dts = [nova.upload(np.ascontiguousarray(tables[i])) for i in range(n)]
+    s = nova.dev_stream_create()
+    qrows, kvrows = n_q * nova.nh * nova.hd, n_q * nova.kvw
+
+    def run():
+        for i in range(n):
+            nova.launch_kv_store_paged(fx.k.ptr, fx.v.ptr, dts[i].ptr, LAYERS[1], fx.nb, n_q, n_past[i],
+                                       kc.ptr + i * kvrows * 2, vc.ptr + i * kvrows * 2, s)
+            nova.launch_attn_prefill_paged(q.ptr + i * qrows * 4, fx.k.ptr, fx.v.ptr, dts[i].ptr, LAYERS[1], fx.nb,
+                                           n_q, n_past[i], o.ptr + i * qrows * 4, s)
+
+    eager, outs = _replays(nova, s, run, lambda: o.numpy((n, n_q, nova.nh, nova.hd), np.float32))
+    assert np.all(np.isfinite(eager))
+    for r, got in enumerate(outs):
+        assert np.array_equal(got.view(np.uint32), eager.view(np.uint32)), f"replay {r}"
+
 def test_gemv_fused_graph(nova7):
     """quantise-in-launch GEMV over three matrices, and the four-token GEMV"""
     nova = nova7
